@@ -1,0 +1,282 @@
+#!/usr/bin/env python3
+"""Benchmark of the LTHC interface forward on one MI355X.
+
+One step is one pass of the interface over one synthetic batch at the metric
+shape (B=256, 64x64 high-res grid, 16x16 workspace, C=768, L=12, bf16
+activations, fp32 weights), with every input resident in HBM before timing:
+
+    Z_0 = R(X_0)                              jit_thc::local_write_traceable
+    gamma_l = sum_k alpha * beta_l  (all l)    jit_thc::lazy_gamma_stack
+    Z_{l+1} = Z_l + gamma_l * dZ_l  (l < 12)   jit_thc::lazy_workspace_update
+    X_L = X_0 + sum_l P_l(dZ_l)                jit_thc::final_accumulate_b4_12_traceable
+
+The dZ_l stand in for the transformer branch outputs (out of scope), so they
+are inputs.  `value` is algorithmic bytes per step / time per step, with the
+per-op compulsory byte count e*(3T + (4L+1)W) + weights (each op reads each
+input once and writes each output once; e = 2, T = B*64*64*C, W = B*256*C).
+
+Prints one JSON line.  `roofline` covers the dominant kernel (the
+materialisation), timed with HIP events around each of its launches on the
+stream it runs on; `cpu_baseline` times the C oracle (oracle/lthc_oracle.c,
+OpenMP) on a bounded slice of the same workload on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+METRIC = "read/write/materialise HBM GB/s (% of 8 TB/s) at B=256 C=768 bf16; fwd img/s"
+PEAK_HBM = 8.0e12
+PMC_PROFILE = os.path.join(ROOT, "profiles", "materialise_fwd_b256_pmc.txt")
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--batch", type=int, default=256)
+    p.add_argument("--channels", type=int, default=768)
+    p.add_argument("--depth", type=int, default=12)
+    p.add_argument("--grid", type=int, default=16, help="workspace grid side (high-res side = 4x)")
+    p.add_argument("--mode", choices=["graph", "eager"], default="graph", help="how `value` is timed")
+    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def algorithmic_bytes(B, G, C, L, e=2):
+    T = B * (4 * G) ** 2 * C
+    W = B * G * G * C
+    read = e * (T + W) + 4 * 16 * C
+    recur = e * 3 * L * W + 4 * L * C  # + gamma vector per step
+    gamma = 4 * 16 * C * (L + 1) + 4 * L * C
+    mat = e * (2 * T + L * W) + 4 * 16 * C * L
+    return {"read": read, "gamma": gamma, "recur": recur, "materialise": mat, "total": read + gamma + recur + mat}
+
+
+def pmc_traffic():
+    """HBM bytes per materialise launch from the committed rocprofv3 --pmc summary, if any."""
+    if not os.path.exists(PMC_PROFILE):
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(PMC_PROFILE).read())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(G, C, L, budget_s):
+    """The C oracle on a slice of the same workload (fp32, OpenMP on the host cores)."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+
+    from oracle import oracle as O
+
+    if not os.path.exists(O.LIB):
+        O.build()
+    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    O.set_threads(threads)
+    Bs = 8
+    d = O.make_inputs(Bs, G, C, L, seed=0)
+    x0, alpha = d["x0"], d["alpha"]
+    betas, dzs = list(d["beta"]), list(d["dz"])
+    rows = Bs * G * G
+
+    def step():
+        z = O.Cread(x0, alpha, G)
+        gam = O.Cgamma(alpha, betas)
+        for l in range(L):
+            z = O.Crecur(z, dzs[l], gam[l])
+        return O.Cwrite(x0, dzs, betas)
+
+    step()  # warm caches and the OpenMP pool
+    n, t0 = 0, time.perf_counter()
+    while True:
+        step()
+        n += 1
+        if time.perf_counter() - t0 >= budget_s or n >= 200:
+            break
+    dt = (time.perf_counter() - t0) / n
+    del rows
+    nbytes = algorithmic_bytes(Bs, G, C, L)["total"]
+    return {
+        "value": round(nbytes / dt / 1e9, 3),
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"C oracle (oracle/lthc_oracle.c, fp32 in/out, fp64 accumulate, OpenMP {threads} threads) running the same "
+            f"step (read, gamma, {L} recurrence steps, materialise) on a B={Bs} slice of the workload; {n} steps in "
+            f"{dt * n:.1f} s; value = the bf16 algorithmic bytes of that slice / time per step"
+        ),
+        "ms_per_step_sample": round(dt * 1e3, 3),
+    }
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(
+            f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the interface shards along the "
+            "batch; see DESIGN.md for the multi-GPU plan)",
+            file=sys.stderr,
+        )
+        sys.exit(2)
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from flowmatching_lthc_amd import ops
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    B, G, C, L = args.batch, args.grid, args.channels, args.depth
+    H = 4 * G
+    bf16 = torch.bfloat16
+
+    gen = torch.Generator(device=dev).manual_seed(0)
+
+    def make_set():
+        x0 = torch.randn((B, H, H, C), generator=gen, device=dev).to(bf16)
+        dzs = [(torch.randn((B, G * G, C), generator=gen, device=dev) * 0.02).to(bf16) for _ in range(L)]
+        return x0, dzs
+
+    alpha = torch.randn((C, 16), generator=gen, device=dev) * 0.01 + 1.0 / 16.0
+    beta_stack = torch.randn((L, C, 16), generator=gen, device=dev) * 0.02
+    betas = list(beta_stack.unbind(0))
+    sets = [make_set(), make_set()]  # rotate two input sets so the 256 MB MALL cannot serve repeats
+    torch.cuda.synchronize()
+
+    stream = torch.cuda.current_stream()
+    mat_events = []
+
+    def step(i, timed=False):
+        x0, dzs = sets[i % 2]
+        z = ops.local_write_traceable(x0, alpha)
+        gam = ops.lazy_gamma_stack(alpha, beta_stack)
+        for l in range(L):
+            z = ops.lazy_workspace_update(z, dzs[l], gam[l])
+        if timed:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+        if L == 12:
+            xl = ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas)
+        else:
+            xl = ops.final_accumulate_b4_traceable(x0, torch.stack(dzs), beta_stack)
+        if timed:
+            e1.record(stream)
+            mat_events.append((e0, e1))
+        return z, xl
+
+    # eager: warmup, then K timed steps with events around every materialise launch
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(args.steps):
+        step(i, timed=True)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    eager_ms = t0.elapsed_time(t1) / args.steps
+    mat_ms = sum(a.elapsed_time(b) for a, b in mat_events) / len(mat_events)
+
+    # graph: one captured step per input set, replayed
+    graph_ms = None
+    graphs = []
+    if args.mode == "graph":
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for i in range(2):
+                step(i)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        outs = []
+        for i in range(2):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                outs.append(step(i))
+            graphs.append(g)
+        ref = step(0)
+        for i in range(max(2, args.warmup)):
+            graphs[i % 2].replay()
+        torch.cuda.synchronize()
+        graphs[0].replay()
+        torch.cuda.synchronize()
+        if not (torch.equal(outs[0][1], ref[1]) and torch.equal(outs[0][0], ref[0])):
+            print("graph replay differs from the eager step", file=sys.stderr)
+            sys.exit(3)
+        t0.record(stream)
+        for i in range(args.steps):
+            graphs[i % 2].replay()
+        t1.record(stream)
+        torch.cuda.synchronize()
+        graph_ms = t0.elapsed_time(t1) / args.steps
+
+    ms = graph_ms if graph_ms is not None else eager_ms
+    nbytes = algorithmic_bytes(B, G, C, L)
+    value = nbytes["total"] / (ms * 1e-3) / 1e9
+    mat_achieved = nbytes["materialise"] / (mat_ms * 1e-3)
+    traffic = pmc_traffic()
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline(G, C, L, args.cpu_seconds)
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "lthc_interface_fwd (read + gamma + L recurrence steps + materialise)",
+            "B": B,
+            "high_grid": H,
+            "workspace_grid": G,
+            "C": C,
+            "L": L,
+            "weights": "fp32",
+            "timing": f"{args.mode} ({'one HIP graph per step' if args.mode == 'graph' else 'eager op launches'})",
+            "bytes_per_step": nbytes["total"],
+            "byte_definition": "per-op compulsory: e*(3T+(4L+1)W) + weights, e=2",
+            "pct_of_peak_hbm": round(100.0 * value * 1e9 / PEAK_HBM, 2),
+        },
+        "roofline": {
+            "kernel": "materialise_kernel<bf16, L=12> (jit_thc::final_accumulate_b4_12_traceable)",
+            "bound": "hbm",
+            "achieved": round(mat_achieved / 1e9, 2),
+            "peak": PEAK_HBM / 1e9,
+            "unit": "GB/s",
+            "frac": round(mat_achieved / PEAK_HBM, 4),
+            "traffic": traffic,
+            "algorithmic_bytes_per_launch": nbytes["materialise"],
+            "avg_launch_ms": round(mat_ms, 4),
+        },
+        "cpu_baseline": cpu,
+        "extra": {
+            "eager_ms_per_step": round(eager_ms, 4),
+            "graph_ms_per_step": None if graph_ms is None else round(graph_ms, 4),
+            "bytes_by_op": nbytes,
+            "device": torch.cuda.get_device_name(0),
+        },
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

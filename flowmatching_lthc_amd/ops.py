@@ -1,0 +1,568 @@
+"""``jit_thc::*`` operators backed by the gfx950 HIP library.
+
+The reference registers its LTHC interface as ``torch.library`` ops in the
+``jit_thc`` namespace (flowmatching_lthc/models/local_thc_triton_kernels.py,
+via ``triton_op`` + ``register_autograd``).  This module registers the same
+names with the same schemas, argument meaning, output dtypes and autograd
+formulas, launching hand-written HIP kernels through the C ABI of
+``include/lthc.h`` instead of Triton.  The reference's ops are fixed to the
+64x64 / 16x16 B/4 geometry; these accept any square grid whose cell side is 4
+(so the 128x128 / 32x32 stress shape runs through the same ops).
+
+Every op:
+  * runs on CUDA (HIP) tensors only and raises ``ValueError`` for CPU tensors,
+    bad shapes, or unsupported dtypes — there is no CPU fallback;
+  * allocates its outputs through torch's caching allocator and launches on
+    ``torch.cuda.current_stream()`` without host synchronisation, so it can be
+    captured in a HIP graph or traced by ``torch.compile`` (``register_fake``);
+  * accumulates in fp32 and rounds once to the output dtype.
+
+Naming follows the reference: the legacy "write" op is the algorithmic READ
+(high-res -> workspace) and the legacy "read" op is the algorithmic WRITE.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Sequence
+
+import torch
+from torch import Tensor
+
+from . import _abi
+
+S = 4  # cell side (taps K = 16)
+K = S * S
+
+
+# ---------------------------------------------------------------------------
+# argument checks
+# ---------------------------------------------------------------------------
+def _on_gpu(*ts: Tensor) -> None:
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise ValueError(f"LTHC HIP ops need GPU tensors, got a {dev} tensor (there is no CPU fallback)")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ValueError(f"all tensors must be on {dev}, got one on {t.device}")
+
+
+def _prep(t: Tensor) -> Tensor:
+    """Contiguous and aligned to 4 elements, as the C ABI requires."""
+    t = t.contiguous()
+    if t.data_ptr() % (4 * t.element_size()) != 0:
+        t = t.clone()
+    return t
+
+
+def _hi_geom(x: Tensor, name: str = "x") -> tuple[int, int, int]:
+    if x.dim() != 4 or x.shape[1] != x.shape[2]:
+        raise ValueError(f"{name} must be NHWC [B,H,H,C], got {tuple(x.shape)}")
+    b, h, _, c = x.shape
+    if h % S != 0:
+        raise ValueError(f"{name}: high-res side {h} is not a multiple of the cell side {S}")
+    if c % 4 != 0:
+        raise ValueError(f"{name}: channels {c} must be a multiple of 4")
+    return b, h // S, c
+
+
+def _lo_geom(z: Tensor, name: str = "z") -> tuple[int, int, int]:
+    if z.dim() != 3:
+        raise ValueError(f"{name} must be [B,M,C], got {tuple(z.shape)}")
+    b, m, c = z.shape
+    g = math.isqrt(m)
+    if g * g != m:
+        raise ValueError(f"{name}: workspace token count {m} is not a square")
+    if c % 4 != 0:
+        raise ValueError(f"{name}: channels {c} must be a multiple of 4")
+    return b, g, c
+
+
+def _check_weight(w: Tensor, c: int, name: str) -> None:
+    if tuple(w.shape) != (c, K):
+        raise ValueError(f"{name} must be [{c},{K}], got {tuple(w.shape)}")
+    _abi.code(w)
+
+
+def _same_dtype(ref: Tensor, others: Sequence[Tensor]) -> list[Tensor]:
+    return [t if t.dtype == ref.dtype else t.to(ref.dtype) for t in others]
+
+
+# ---------------------------------------------------------------------------
+# launches (inputs already checked and prepared)
+# ---------------------------------------------------------------------------
+def _launch_read(x: Tensor, w: Tensor, z: Tensor, b: int, g: int, c: int) -> None:
+    with torch.cuda.device(x.device):
+        rc = _abi.load().lthc_read_fwd(
+            x.data_ptr(), _abi.code(x), w.data_ptr(), _abi.code(w), z.data_ptr(), b, g, S, c, _abi.stream_of(x)
+        )
+    _abi.check(rc, "lthc_read_fwd")
+
+
+def _launch_materialise(base: Tensor | None, dzs: Sequence[Tensor], betas: Sequence[Tensor], out: Tensor) -> None:
+    b, g, c = _lo_geom(dzs[0], "dz")
+    wd = _abi.code(betas[0])
+    with torch.cuda.device(out.device):
+        rc = _abi.load().lthc_materialise_fwd(
+            _abi.ptr(base), _abi.ptr_array(dzs), _abi.code(out), _abi.ptr_array(betas), wd, out.data_ptr(),
+            b, g, S, c, len(dzs), _abi.stream_of(out),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_materialise_fwd")
+
+
+def _launch_read_multi(gr: Tensor, ws: Sequence[Tensor], outs: Sequence[Tensor]) -> None:
+    b, g, c = _hi_geom(gr, "grad_out")
+    with torch.cuda.device(gr.device):
+        rc = _abi.load().lthc_read_multi_fwd(
+            gr.data_ptr(), _abi.code(gr), _abi.ptr_array(ws), _abi.code(ws[0]), _abi.ptr_array(outs),
+            b, g, S, c, len(ws), _abi.stream_of(gr),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_read_multi_fwd")
+
+
+def _launch_weight_grad(high: Tensor, lows: Sequence[Tensor]) -> Tensor:
+    b, g, c = _hi_geom(high, "high")
+    L = len(lows)
+    out = torch.empty((L, c, K), device=high.device, dtype=torch.float32)
+    nbytes = _abi.weight_grad_workspace_bytes(b, g, S, c, L)
+    ws = torch.empty((max(nbytes, 16),), device=high.device, dtype=torch.uint8)
+    with torch.cuda.device(high.device):
+        rc = _abi.load().lthc_weight_grad(
+            high.data_ptr(), _abi.ptr_array(lows), _abi.code(high), out.data_ptr(), b, g, S, c, L,
+            ws.data_ptr(), ws.numel(), _abi.stream_of(high),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_weight_grad")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# READ  (jit_thc::local_write_traceable, local_thc_triton_kernels.py:2673-2683)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("jit_thc::local_write_traceable", mutates_args=())
+def local_write_traceable(x: Tensor, weight: Tensor) -> Tensor:
+    """Z[b,m,c] = sum_k weight[c,k] X[b,m,k,c]: x [B,H,H,C] -> z [B,(H/4)^2,C] in x.dtype."""
+    _on_gpu(x, weight)
+    b, g, c = _hi_geom(x)
+    _check_weight(weight, c, "weight")
+    x, w = _prep(x), _prep(weight)
+    z = torch.empty((b, g * g, c), device=x.device, dtype=x.dtype)
+    _launch_read(x, w, z, b, g, c)
+    return z
+
+
+@local_write_traceable.register_fake
+def _(x: Tensor, weight: Tensor) -> Tensor:
+    b, g, c = _hi_geom(x)
+    return x.new_empty((b, g * g, c))
+
+
+# ---------------------------------------------------------------------------
+# WRITE  (jit_thc::local_read_traceable, local_thc_triton_kernels.py:2686-2696)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("jit_thc::local_read_traceable", mutates_args=())
+def local_read_traceable(z: Tensor, weight: Tensor) -> Tensor:
+    """X[b,m,k,c] = weight[c,k] Z[b,m,c]: z [B,M,C] -> x [B,4*sqrt(M),4*sqrt(M),C] in z.dtype."""
+    _on_gpu(z, weight)
+    b, g, c = _lo_geom(z)
+    _check_weight(weight, c, "weight")
+    z, w = _prep(z), _prep(weight)
+    out = torch.empty((b, g * S, g * S, c), device=z.device, dtype=z.dtype)
+    _launch_materialise(None, [z], [w], out)
+    return out
+
+
+@local_read_traceable.register_fake
+def _(z: Tensor, weight: Tensor) -> Tensor:
+    b, g, c = _lo_geom(z)
+    return z.new_empty((b, g * S, g * S, c))
+
+
+# ---------------------------------------------------------------------------
+# CELL WEIGHT GRADIENT  (jit_thc::local_weight_grad_traceable, :2699-2710)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("jit_thc::local_weight_grad_traceable", mutates_args=())
+def local_weight_grad_traceable(high: Tensor, low: Tensor) -> Tensor:
+    """gW[c,k] = sum_{b,m} high[b,m,k,c] low[b,m,c] in fp32 [C,16] (deterministic order)."""
+    _on_gpu(high, low)
+    b, g, c = _hi_geom(high, "high")
+    bl, gl, cl = _lo_geom(low, "low")
+    if (bl, gl, cl) != (b, g, c):
+        raise ValueError(f"high {tuple(high.shape)} and low {tuple(low.shape)} do not match")
+    high = _prep(high)
+    (low,) = _same_dtype(high, [_prep(low)])
+    return _launch_weight_grad(high, [low])[0]
+
+
+@local_weight_grad_traceable.register_fake
+def _(high: Tensor, low: Tensor) -> Tensor:
+    c = high.shape[3]
+    return high.new_empty((c, K), dtype=torch.float32)
+
+
+def _setup_write_ctx(ctx, inputs, output):
+    x, weight = inputs
+    ctx.save_for_backward(x, weight)
+
+
+def _backward_write(ctx, grad_z):
+    # local_thc_triton_kernels.py:2726-2729
+    x, weight = ctx.saved_tensors
+    grad_x = local_read_traceable(grad_z, weight) if ctx.needs_input_grad[0] else None
+    grad_w = local_weight_grad_traceable(x, grad_z).to(dtype=weight.dtype) if ctx.needs_input_grad[1] else None
+    return grad_x, grad_w
+
+
+def _setup_read_ctx(ctx, inputs, output):
+    z, weight = inputs
+    ctx.save_for_backward(z, weight)
+
+
+def _backward_read(ctx, grad_x):
+    # local_thc_triton_kernels.py:2737-2741
+    z, weight = ctx.saved_tensors
+    grad_z = local_write_traceable(grad_x, weight) if ctx.needs_input_grad[0] else None
+    grad_w = local_weight_grad_traceable(grad_x, z).to(dtype=weight.dtype) if ctx.needs_input_grad[1] else None
+    return grad_z, grad_w
+
+
+torch.library.register_autograd(local_write_traceable, _backward_write, setup_context=_setup_write_ctx)
+torch.library.register_autograd(local_read_traceable, _backward_read, setup_context=_setup_read_ctx)
+
+
+# ---------------------------------------------------------------------------
+# MATERIALISE, stacked form (jit_thc::final_accumulate_b4_traceable, :1578-1666)
+# ---------------------------------------------------------------------------
+def _check_stack(x0: Tensor, dz_stack: Tensor, beta_stack: Tensor) -> tuple[int, int, int, int]:
+    b, g, c = _hi_geom(x0, "x0")
+    if dz_stack.dim() != 4 or tuple(dz_stack.shape[1:]) != (b, g * g, c):
+        raise ValueError(f"dz_stack must be [L,{b},{g * g},{c}], got {tuple(dz_stack.shape)}")
+    L = dz_stack.shape[0]
+    if tuple(beta_stack.shape) != (L, c, K):
+        raise ValueError(f"beta_stack must be [{L},{c},{K}], got {tuple(beta_stack.shape)}")
+    if not 1 <= L <= _abi.MAX_LAYERS:
+        raise ValueError(f"depth {L} outside 1..{_abi.MAX_LAYERS}")
+    return b, g, c, L
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_b4_traceable", mutates_args=())
+def final_accumulate_b4_traceable(x0: Tensor, dz_stack: Tensor, beta_stack: Tensor) -> Tensor:
+    """X_L = x0 + sum_l beta_stack[l][c,k] dz_stack[l][b,m,c] in x0.dtype."""
+    _on_gpu(x0, dz_stack, beta_stack)
+    _check_stack(x0, dz_stack, beta_stack)
+    x0 = _prep(x0)
+    (dz_stack,) = _same_dtype(x0, [_prep(dz_stack)])
+    beta_stack = _prep(beta_stack)
+    out = torch.empty_like(x0)
+    _launch_materialise(x0, list(dz_stack.unbind(0)), list(beta_stack.unbind(0)), out)
+    return out
+
+
+@final_accumulate_b4_traceable.register_fake
+def _(x0: Tensor, dz_stack: Tensor, beta_stack: Tensor) -> Tensor:
+    return torch.empty_like(x0)
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_b4_grad_dz", mutates_args=())
+def final_accumulate_b4_grad_dz_traceable(grad_out: Tensor, beta_stack: Tensor) -> Tensor:
+    """gdZ[l,b,m,c] = sum_k beta_stack[l][c,k] grad_out[b,m,k,c] in grad_out.dtype ([L,B,M,C])."""
+    _on_gpu(grad_out, beta_stack)
+    b, g, c = _hi_geom(grad_out, "grad_out")
+    L = beta_stack.shape[0]
+    if beta_stack.dim() != 3 or tuple(beta_stack.shape[1:]) != (c, K) or not 1 <= L <= _abi.MAX_LAYERS:
+        raise ValueError(f"beta_stack must be [L,{c},{K}] with 1 <= L <= {_abi.MAX_LAYERS}, got {tuple(beta_stack.shape)}")
+    grad_out, beta_stack = _prep(grad_out), _prep(beta_stack)
+    gdz = torch.empty((L, b, g * g, c), device=grad_out.device, dtype=grad_out.dtype)
+    _launch_read_multi(grad_out, list(beta_stack.unbind(0)), list(gdz.unbind(0)))
+    return gdz
+
+
+@final_accumulate_b4_grad_dz_traceable.register_fake
+def _(grad_out: Tensor, beta_stack: Tensor) -> Tensor:
+    b, g, c = _hi_geom(grad_out, "grad_out")
+    return grad_out.new_empty((beta_stack.shape[0], b, g * g, c))
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_b4_grad_beta", mutates_args=())
+def final_accumulate_b4_grad_beta_traceable(grad_out: Tensor, dz_stack: Tensor, beta_stack: Tensor) -> Tensor:
+    """gbeta[l,c,k] = sum_{b,m} grad_out[b,m,k,c] dz_stack[l][b,m,c] in fp32 [L,C,16]."""
+    _on_gpu(grad_out, dz_stack, beta_stack)
+    _check_stack(grad_out, dz_stack, beta_stack)
+    grad_out = _prep(grad_out)
+    (dz_stack,) = _same_dtype(grad_out, [_prep(dz_stack)])
+    return _launch_weight_grad(grad_out, list(dz_stack.unbind(0)))
+
+
+@final_accumulate_b4_grad_beta_traceable.register_fake
+def _(grad_out: Tensor, dz_stack: Tensor, beta_stack: Tensor) -> Tensor:
+    return grad_out.new_empty((dz_stack.shape[0], grad_out.shape[3], K), dtype=torch.float32)
+
+
+def _setup_final_accumulate_ctx(ctx, inputs, output):
+    _, dz_stack, beta_stack = inputs
+    ctx.save_for_backward(dz_stack, beta_stack)
+
+
+def _backward_final_accumulate(ctx, grad_out):
+    # local_thc_triton_kernels.py:1652-1660: grad_x0 is grad_out itself.
+    dz_stack, beta_stack = ctx.saved_tensors
+    grad_out = grad_out.contiguous()
+    grad_dz = final_accumulate_b4_grad_dz_traceable(grad_out, beta_stack) if ctx.needs_input_grad[1] else None
+    grad_beta = None
+    if ctx.needs_input_grad[2]:
+        grad_beta = final_accumulate_b4_grad_beta_traceable(grad_out, dz_stack, beta_stack).to(dtype=beta_stack.dtype)
+    return grad_out, grad_dz, grad_beta
+
+
+torch.library.register_autograd(
+    final_accumulate_b4_traceable, _backward_final_accumulate, setup_context=_setup_final_accumulate_ctx
+)
+
+
+# ---------------------------------------------------------------------------
+# MATERIALISE, 12 separate layers (jit_thc::final_accumulate_b4_12_traceable,
+# local_thc_triton_kernels.py:1669-1736) and its backward ops (:1800-1919)
+# ---------------------------------------------------------------------------
+def _check_12(x0: Tensor, dzs: Sequence[Tensor], betas: Sequence[Tensor]) -> None:
+    b, g, c = _hi_geom(x0, "x0")
+    for i, dz in enumerate(dzs):
+        if tuple(dz.shape) != (b, g * g, c):
+            raise ValueError(f"dz{i} must be [{b},{g * g},{c}], got {tuple(dz.shape)}")
+    for i, bt in enumerate(betas):
+        _check_weight(bt, c, f"beta{i}")
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_b4_12_traceable", mutates_args=())
+def final_accumulate_b4_12_traceable(
+    x0: Tensor,
+    dz0: Tensor, dz1: Tensor, dz2: Tensor, dz3: Tensor, dz4: Tensor, dz5: Tensor,
+    dz6: Tensor, dz7: Tensor, dz8: Tensor, dz9: Tensor, dz10: Tensor, dz11: Tensor,
+    beta0: Tensor, beta1: Tensor, beta2: Tensor, beta3: Tensor, beta4: Tensor, beta5: Tensor,
+    beta6: Tensor, beta7: Tensor, beta8: Tensor, beta9: Tensor, beta10: Tensor, beta11: Tensor,
+) -> Tensor:  # fmt: skip
+    """X_L = x0 + sum_{l<12} beta_l[c,k] dz_l[b,m,c]; one pass over X0, stored once in x0.dtype."""
+    dzs = [dz0, dz1, dz2, dz3, dz4, dz5, dz6, dz7, dz8, dz9, dz10, dz11]
+    betas = [beta0, beta1, beta2, beta3, beta4, beta5, beta6, beta7, beta8, beta9, beta10, beta11]
+    _on_gpu(x0, *dzs, *betas)
+    _check_12(x0, dzs, betas)
+    x0 = _prep(x0)
+    dzs = _same_dtype(x0, [_prep(d) for d in dzs])
+    betas = [_prep(bt) for bt in betas]
+    if len({bt.dtype for bt in betas}) != 1:
+        betas = [bt.float() for bt in betas]
+    out = torch.empty_like(x0)
+    _launch_materialise(x0, dzs, betas, out)
+    return out
+
+
+@final_accumulate_b4_12_traceable.register_fake
+def _(x0, *rest):
+    return torch.empty_like(x0)
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_b4_12_grad_dz_ptr", mutates_args=())
+def final_accumulate_b4_12_grad_dz_ptr_traceable(
+    grad_out: Tensor,
+    beta0: Tensor, beta1: Tensor, beta2: Tensor, beta3: Tensor, beta4: Tensor, beta5: Tensor,
+    beta6: Tensor, beta7: Tensor, beta8: Tensor, beta9: Tensor, beta10: Tensor, beta11: Tensor,
+) -> Tensor:  # fmt: skip
+    """[12,B,M,C] stack of gdZ_l = sum_k beta_l[c,k] grad_out[b,m,k,c] in grad_out.dtype."""
+    betas = [beta0, beta1, beta2, beta3, beta4, beta5, beta6, beta7, beta8, beta9, beta10, beta11]
+    _on_gpu(grad_out, *betas)
+    b, g, c = _hi_geom(grad_out, "grad_out")
+    for i, bt in enumerate(betas):
+        _check_weight(bt, c, f"beta{i}")
+    grad_out = _prep(grad_out)
+    betas = [_prep(bt) for bt in betas]
+    if len({bt.dtype for bt in betas}) != 1:
+        betas = [bt.float() for bt in betas]
+    gdz = torch.empty((12, b, g * g, c), device=grad_out.device, dtype=grad_out.dtype)
+    _launch_read_multi(grad_out, betas, list(gdz.unbind(0)))
+    return gdz
+
+
+@final_accumulate_b4_12_grad_dz_ptr_traceable.register_fake
+def _(grad_out, *betas):
+    b, g, c = _hi_geom(grad_out, "grad_out")
+    return grad_out.new_empty((12, b, g * g, c))
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_b4_12_grad_beta_ptr", mutates_args=())
+def final_accumulate_b4_12_grad_beta_ptr_traceable(
+    grad_out: Tensor,
+    dz0: Tensor, dz1: Tensor, dz2: Tensor, dz3: Tensor, dz4: Tensor, dz5: Tensor,
+    dz6: Tensor, dz7: Tensor, dz8: Tensor, dz9: Tensor, dz10: Tensor, dz11: Tensor,
+) -> Tensor:  # fmt: skip
+    """fp32 [12,C,16] stack of gbeta_l = sum_{b,m} grad_out[b,m,k,c] dz_l[b,m,c] (deterministic)."""
+    dzs = [dz0, dz1, dz2, dz3, dz4, dz5, dz6, dz7, dz8, dz9, dz10, dz11]
+    _on_gpu(grad_out, *dzs)
+    b, g, c = _hi_geom(grad_out, "grad_out")
+    for i, dz in enumerate(dzs):
+        if tuple(dz.shape) != (b, g * g, c):
+            raise ValueError(f"dz{i} must be [{b},{g * g},{c}], got {tuple(dz.shape)}")
+    grad_out = _prep(grad_out)
+    dzs = _same_dtype(grad_out, [_prep(d) for d in dzs])
+    return _launch_weight_grad(grad_out, dzs)
+
+
+@final_accumulate_b4_12_grad_beta_ptr_traceable.register_fake
+def _(grad_out, *dzs):
+    return grad_out.new_empty((12, grad_out.shape[3], K), dtype=torch.float32)
+
+
+def _setup_final_accumulate_12_ctx(ctx, inputs, output):
+    ctx.save_for_backward(*inputs[1:])
+
+
+def _backward_final_accumulate_12(ctx, grad_out):
+    # local_thc_triton_kernels.py:1901-1912: grad_x0 is grad_out itself.
+    saved = ctx.saved_tensors
+    dzs, betas = saved[:12], saved[12:]
+    grad_out = grad_out.contiguous()
+    need = ctx.needs_input_grad
+    grad_dzs = (None,) * 12
+    grad_betas = (None,) * 12
+    if any(need[1:13]):
+        grad_dzs = tuple(final_accumulate_b4_12_grad_dz_ptr_traceable(grad_out, *betas).unbind(0))
+    if any(need[13:25]):
+        gb = final_accumulate_b4_12_grad_beta_ptr_traceable(grad_out, *dzs)
+        grad_betas = tuple(g.to(dtype=bt.dtype) for g, bt in zip(gb.unbind(0), betas, strict=True))
+    return (grad_out, *grad_dzs, *grad_betas)
+
+
+torch.library.register_autograd(
+    final_accumulate_b4_12_traceable, _backward_final_accumulate_12, setup_context=_setup_final_accumulate_12_ctx
+)
+
+
+# ---------------------------------------------------------------------------
+# LAZY WORKSPACE RECURRENCE  (no reference op: local_thc.py:1325-1328 is eager torch)
+# ---------------------------------------------------------------------------
+def _check_recur(z: Tensor, dz: Tensor, gamma: Tensor) -> int:
+    if z.shape != dz.shape or z.dim() < 1:
+        raise ValueError(f"z {tuple(z.shape)} and dz {tuple(dz.shape)} must have the same shape")
+    c = z.shape[-1]
+    if tuple(gamma.shape) != (c,):
+        raise ValueError(f"gamma must be [{c}], got {tuple(gamma.shape)}")
+    if c % 4 != 0:
+        raise ValueError(f"channels {c} must be a multiple of 4")
+    _abi.code(gamma)
+    return c
+
+
+@torch.library.custom_op("jit_thc::lazy_workspace_update", mutates_args=())
+def lazy_workspace_update(z: Tensor, dz: Tensor, gamma: Tensor) -> Tensor:
+    """Z_{l+1} = Z_l + gamma[c] * dZ_l computed as fma(gamma, dz, z), in the promoted dtype of z and dz."""
+    _on_gpu(z, dz, gamma)
+    c = _check_recur(z, dz, gamma)
+    dt = torch.promote_types(z.dtype, dz.dtype)
+    z, dz, gamma = _prep(z.to(dt)), _prep(dz.to(dt)), _prep(gamma)
+    out = torch.empty_like(z)
+    with torch.cuda.device(z.device):
+        rc = _abi.load().lthc_recur_fwd(
+            z.data_ptr(), dz.data_ptr(), _abi.code(z), gamma.data_ptr(), _abi.code(gamma), out.data_ptr(),
+            z.numel() // c, c, _abi.stream_of(z),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_recur_fwd")
+    return out
+
+
+@lazy_workspace_update.register_fake
+def _(z: Tensor, dz: Tensor, gamma: Tensor) -> Tensor:
+    return z.new_empty(z.shape, dtype=torch.promote_types(z.dtype, dz.dtype))
+
+
+@torch.library.custom_op("jit_thc::lazy_workspace_update_backward", mutates_args=())
+def lazy_workspace_update_backward(grad: Tensor, dz: Tensor, gamma: Tensor) -> tuple[Tensor, Tensor]:
+    """(gamma * grad in grad.dtype, fp32 [C] sum over rows of grad * dz)."""
+    _on_gpu(grad, dz, gamma)
+    c = _check_recur(grad, dz, gamma)
+    grad = _prep(grad)
+    (dz,) = _same_dtype(grad, [_prep(dz)])
+    gamma = _prep(gamma)
+    rows = grad.numel() // c
+    gdz = torch.empty_like(grad)
+    ggamma = torch.empty((c,), device=grad.device, dtype=torch.float32)
+    ws = torch.empty((max(_abi.recur_bwd_workspace_bytes(rows, c), 16),), device=grad.device, dtype=torch.uint8)
+    with torch.cuda.device(grad.device):
+        rc = _abi.load().lthc_recur_bwd(
+            grad.data_ptr(), dz.data_ptr(), _abi.code(grad), gamma.data_ptr(), _abi.code(gamma), gdz.data_ptr(),
+            ggamma.data_ptr(), rows, c, ws.data_ptr(), ws.numel(), _abi.stream_of(grad),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_recur_bwd")
+    return gdz, ggamma
+
+
+@lazy_workspace_update_backward.register_fake
+def _(grad: Tensor, dz: Tensor, gamma: Tensor):
+    return torch.empty_like(grad), grad.new_empty((grad.shape[-1],), dtype=torch.float32)
+
+
+def _setup_recur_ctx(ctx, inputs, output):
+    _, dz, gamma = inputs
+    ctx.save_for_backward(dz, gamma)
+    ctx.z_dtype = inputs[0].dtype
+
+
+def _backward_recur(ctx, grad):
+    dz, gamma = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    grad_z = grad.to(ctx.z_dtype) if need[0] else None
+    grad_dz = grad_gamma = None
+    if need[1] or need[2]:
+        gdz, gg = lazy_workspace_update_backward(grad, dz, gamma)
+        grad_dz = gdz.to(dz.dtype) if need[1] else None
+        grad_gamma = gg.to(gamma.dtype) if need[2] else None
+    return grad_z, grad_dz, grad_gamma
+
+
+torch.library.register_autograd(lazy_workspace_update, _backward_recur, setup_context=_setup_recur_ctx)
+
+
+# ---------------------------------------------------------------------------
+# GAMMA STACK  gamma[l,c] = sum_k alpha[c,k] beta_stack[l,c,k]  (fp32)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("jit_thc::lazy_gamma_stack", mutates_args=())
+def lazy_gamma_stack(alpha: Tensor, beta_stack: Tensor) -> Tensor:
+    """fp32 [L,C] of gamma_l = sum_k alpha * beta_l (LayerLocalWrite.gamma_from_alpha for all layers)."""
+    _on_gpu(alpha, beta_stack)
+    if alpha.dim() != 2 or beta_stack.dim() != 3 or tuple(beta_stack.shape[1:]) != tuple(alpha.shape):
+        raise ValueError(f"alpha [C,K] and beta_stack [L,C,K] expected, got {tuple(alpha.shape)}, {tuple(beta_stack.shape)}")
+    L = beta_stack.shape[0]
+    if not 1 <= L <= _abi.MAX_LAYERS:
+        raise ValueError(f"depth {L} outside 1..{_abi.MAX_LAYERS}")
+    (beta_stack,) = _same_dtype(alpha, [beta_stack])
+    alpha, beta_stack = alpha.contiguous(), beta_stack.contiguous()
+    c, k = alpha.shape
+    out = torch.empty((L, c), device=alpha.device, dtype=torch.float32)
+    with torch.cuda.device(alpha.device):
+        rc = _abi.load().lthc_gamma(
+            alpha.data_ptr(), _abi.ptr_array(list(beta_stack.unbind(0))), _abi.code(alpha), out.data_ptr(),
+            _abi.F32, c, k, L, _abi.stream_of(alpha),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_gamma")
+    return out
+
+
+@lazy_gamma_stack.register_fake
+def _(alpha: Tensor, beta_stack: Tensor) -> Tensor:
+    return alpha.new_empty((beta_stack.shape[0], alpha.shape[0]), dtype=torch.float32)
+
+
+def _setup_gamma_ctx(ctx, inputs, output):
+    ctx.save_for_backward(*inputs)
+
+
+def _backward_gamma(ctx, grad):
+    alpha, beta_stack = ctx.saved_tensors
+    g = grad.float()
+    grad_alpha = (g[:, :, None] * beta_stack.float()).sum(0).to(alpha.dtype) if ctx.needs_input_grad[0] else None
+    grad_beta = (g[:, :, None] * alpha.float()[None]).to(beta_stack.dtype) if ctx.needs_input_grad[1] else None
+    return grad_alpha, grad_beta
+
+
+torch.library.register_autograd(lazy_gamma_stack, _backward_gamma, setup_context=_setup_gamma_ctx)
+
+
+# Reference-style aliases (local_thc_triton_kernels.py exports these names).
+triton_final_accumulate_b4_traceable = final_accumulate_b4_traceable
+triton_final_accumulate_b4_12_traceable = final_accumulate_b4_12_traceable

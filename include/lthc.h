@@ -1,0 +1,157 @@
+/*
+ * lthc.h — C ABI of the MI355X (gfx950) Local Token Hyper-Connection interface.
+ *
+ * The library replaces the device side of the reference's LTHC interface: the
+ * shared channel-wise read from the high-resolution NHWC residual stream into
+ * the workspace, the per-layer channel-wise write with its lazy workspace
+ * recurrence, and the single final materialisation, forward and backward.
+ * The reference exposes these as torch.library ops (namespace `jit_thc`) in
+ * flowmatching_lthc/models/local_thc_triton_kernels.py and as module hooks in
+ * flowmatching_lthc/models/local_thc.py; each entry point below names the
+ * reference op, kernel or hook it replaces.
+ *
+ * Conventions shared by every entry point
+ *   - All tensors are dense, row-major, in device memory of the current HIP
+ *     device.  Pointers must be aligned to 4 elements (8 bytes for 16-bit
+ *     types, 16 bytes for fp32) and C must be a multiple of 4.
+ *   - Geometry: B batch, G workspace grid side, s cell side (taps K = s*s),
+ *     C channels.  High-resolution grid side H = G*s.  Cells M = G*G.
+ *       x  (high-res)  [B, H, H, C]   (NHWC; cell view [B, M, K, C] is logical)
+ *       z  (workspace) [B, M, C]
+ *       w  (weights)   [C, K]         (alpha = read weights, beta_l = write weights)
+ *     Tap k = sy*s + sx of cell m = gy*G + gx lives at h = gy*s + sy,
+ *     w = gx*s + sx (local_thc_triton_kernels.py:355-363).
+ *     Only s == 4 is implemented (K = 16, the B/4 model and the 512px
+ *     stress configuration); other values return LTHC_ERR_UNSUPPORTED.
+ *   - dtype codes: LTHC_F32, LTHC_BF16, LTHC_F16.  Activations share one
+ *     dtype per call; weights carry their own dtype.  All arithmetic is fp32
+ *     (fused multiply-add), results are rounded once (round-to-nearest-even)
+ *     to the output dtype.
+ *   - Every call is asynchronous on `stream` (a hipStream_t; NULL = the null
+ *     stream), performs no host synchronisation and no device allocation.
+ *     Entry points that need scratch memory take a caller-provided workspace
+ *     whose size is given by the matching *_workspace_bytes function.
+ *   - Return value: LTHC_OK (0) or an error code; lthc_last_error() then
+ *     returns a thread-local description.  A call with an empty batch
+ *     (B == 0 or rows == 0) is a no-op that returns LTHC_OK (the weight
+ *     gradients are then written as zeros).
+ */
+#ifndef LTHC_H_
+#define LTHC_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LTHC_F32 0
+#define LTHC_BF16 1
+#define LTHC_F16 2
+
+#define LTHC_OK 0
+#define LTHC_ERR_INVALID 1     /* bad argument: shape, dtype, alignment, null pointer */
+#define LTHC_ERR_UNSUPPORTED 2 /* valid but not implemented (s != 4, L too large) */
+#define LTHC_ERR_HIP 3         /* a HIP runtime call failed (launch error, no device) */
+
+/* Largest depth L accepted by the multi-layer entry points. */
+#define LTHC_MAX_LAYERS 48
+
+/* Thread-local text of the last error raised on this thread ("" if none). */
+const char* lthc_last_error(void);
+
+/* ABI version of this library (incremented on any signature change). */
+int lthc_abi_version(void);
+
+/*
+ * READ   z[b,m,c] = sum_k alpha[c,k] * x[b,m,k,c]
+ * Replaces jit_thc::local_write_traceable (local_thc_triton_kernels.py:2673-2683,
+ * kernel _write_fwd_kernel :27-60; the legacy name "write" is the algorithmic
+ * read) and the eager SharedLocalRead.read (local_thc.py:1211-1223).
+ * Accumulation order k = 0..K-1, acc = fma(x, alpha, acc), as in :51-55.
+ */
+int lthc_read_fwd(const void* x, int x_dtype, const void* alpha, int w_dtype, void* z,
+                  int64_t B, int64_t G, int64_t s, int64_t C, void* stream);
+
+/*
+ * MULTI-WEIGHT READ   out_l[b,m,c] = sum_k w_l[c,k] * g[b,m,k,c],  l < L
+ * Replaces jit_thc::final_accumulate_b4_12_grad_dz_ptr
+ * (local_thc_triton_kernels.py:1800-1845, kernel :512-595) and
+ * jit_thc::final_accumulate_b4_grad_dz (:1601-1621, kernel :241-277): the
+ * gradient of the materialisation with respect to each dZ_l.
+ * `w` and `out` are host arrays of L device pointers.
+ */
+int lthc_read_multi_fwd(const void* g, int x_dtype, const void* const* w, int w_dtype,
+                        void* const* out, int64_t B, int64_t G, int64_t s, int64_t C, int L,
+                        void* stream);
+
+/*
+ * MATERIALISE / WRITE
+ *   out[b,m,k,c] = base[b,m,k,c] + sum_{l<L} beta_l[c,k] * dz_l[b,m,c]
+ * `base` may be NULL (treated as zero).  `dz` and `beta` are host arrays of L
+ * device pointers ([B,M,C] and [C,K]).  Accumulation: acc = base, then
+ * acc = fma(beta_l, dz_l, acc) for l = 0..L-1, one rounding at the store.
+ * Replaces
+ *   jit_thc::final_accumulate_b4_12_traceable (local_thc_triton_kernels.py:1669-1736,
+ *     kernel _final_accumulate_b4_12_fwd_kernel :317-405)            base = x0, L = 12
+ *   jit_thc::final_accumulate_b4_traceable (:1578-1598, kernel :202-238)  any L
+ *   jit_thc::local_read_traceable (:2686-2696, kernel _read_fwd_kernel :63-95)
+ *     and the read backward dX = R^T gZ (:1409, :2726-2729)         base = NULL, L = 1
+ *   LayerLocalWrite.write / write_add (local_thc.py:1261-1276) and the
+ *     final_accumulate_reference loop (local_thc.py:1368-1372).
+ */
+int lthc_materialise_fwd(const void* base, const void* const* dz, int x_dtype,
+                         const void* const* beta, int w_dtype, void* out,
+                         int64_t B, int64_t G, int64_t s, int64_t C, int L, void* stream);
+
+/*
+ * CELL WEIGHT GRADIENT (deterministic two-stage fp32 reduction)
+ *   gw[l,c,k] = sum_{b,m} high[b,m,k,c] * low_l[b,m,c]      gw: fp32 [L,C,K]
+ * Replaces jit_thc::local_weight_grad_traceable (local_thc_triton_kernels.py:2699-2710,
+ * kernel _cell_weight_grad_kernel :167-199) — d(alpha) of the read with
+ * high = x, low = gZ, and d(weight) of the write with high = gX, low = z —
+ * and jit_thc::final_accumulate_b4_12_grad_beta_ptr (:1848-1894, kernel :598-680),
+ * jit_thc::final_accumulate_b4_grad_beta (:1624-1644): d(beta_l) of the
+ * materialisation with high = grad_out, low_l = dz_l.  The reference reduces
+ * with relaxed fp32 atomics; this library sums per-block partials in a fixed
+ * order, so results are bitwise reproducible run to run.
+ */
+size_t lthc_weight_grad_workspace_bytes(int64_t B, int64_t G, int64_t s, int64_t C, int L);
+int lthc_weight_grad(const void* high, const void* const* low, int x_dtype, float* gw,
+                     int64_t B, int64_t G, int64_t s, int64_t C, int L,
+                     void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * GAMMA   gamma_l[c] = sum_k alpha[c,k] * beta_l[c,k]   (written in out_dtype)
+ * Replaces LayerLocalWrite.gamma_from_alpha (local_thc.py:1278-1283), computed
+ * here in fp32 from the given weights.  `beta` is a host array of L device
+ * pointers; `gamma` is [L,C].
+ */
+int lthc_gamma(const void* alpha, const void* const* beta, int w_dtype, void* gamma, int out_dtype,
+               int64_t C, int64_t K, int L, void* stream);
+
+/*
+ * LAZY WORKSPACE RECURRENCE STEP   z_next[r,c] = z[r,c] + gamma[c] * dz[r,c]
+ * Replaces SharedReadLocalTHCSharedAdaLNJiTBlock.lazy_workspace_update
+ * (local_thc.py:1325-1328); rows = B*M.  Computed as fma(gamma, dz, z).
+ */
+int lthc_recur_fwd(const void* z, const void* dz, int x_dtype, const void* gamma, int g_dtype,
+                   void* z_next, int64_t rows, int64_t C, void* stream);
+
+/*
+ * RECURRENCE BACKWARD (given g = dL/dz_next)
+ *   gdz[r,c]   = gamma[c] * g[r,c]                 (x_dtype)
+ *   ggamma[c]  = sum_r g[r,c] * dz[r,c]            (fp32, deterministic)
+ * dL/dz = g itself, as in eager autograd of local_thc.py:1328.
+ */
+size_t lthc_recur_bwd_workspace_bytes(int64_t rows, int64_t C);
+int lthc_recur_bwd(const void* g, const void* dz, int x_dtype, const void* gamma, int g_dtype,
+                   void* gdz, float* ggamma, int64_t rows, int64_t C,
+                   void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LTHC_H_ */

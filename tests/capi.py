@@ -1,0 +1,96 @@
+"""Direct C-ABI calls for the GPU parity tests (torch only allocates memory)."""
+
+from __future__ import annotations
+
+import torch
+
+from flowmatching_lthc_amd import _abi
+
+S = 4
+
+
+def _lib():
+    return _abi.load()
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def read(x: torch.Tensor, alpha: torch.Tensor) -> torch.Tensor:
+    b, h, _, c = x.shape
+    g = h // S
+    z = torch.empty((b, g * g, c), device=x.device, dtype=x.dtype)
+    rc = _lib().lthc_read_fwd(x.data_ptr(), _abi.code(x), alpha.data_ptr(), _abi.code(alpha), z.data_ptr(), b, g, S, c, _stream())
+    _abi.check(rc, "lthc_read_fwd")
+    return z
+
+
+def materialise(base, dzs, betas, h=None) -> torch.Tensor:
+    b, m, c = dzs[0].shape
+    g = int(round(m**0.5))
+    h = g * S
+    out = torch.empty((b, h, h, c), device=dzs[0].device, dtype=dzs[0].dtype)
+    rc = _lib().lthc_materialise_fwd(
+        _abi.ptr(base), _abi.ptr_array(dzs), _abi.code(dzs[0]), _abi.ptr_array(betas), _abi.code(betas[0]),
+        out.data_ptr(), b, g, S, c, len(dzs), _stream(),
+    )  # fmt: skip
+    _abi.check(rc, "lthc_materialise_fwd")
+    return out
+
+
+def read_multi(gr: torch.Tensor, ws) -> list[torch.Tensor]:
+    b, h, _, c = gr.shape
+    g = h // S
+    outs = [torch.empty((b, g * g, c), device=gr.device, dtype=gr.dtype) for _ in ws]
+    rc = _lib().lthc_read_multi_fwd(
+        gr.data_ptr(), _abi.code(gr), _abi.ptr_array(ws), _abi.code(ws[0]), _abi.ptr_array(outs), b, g, S, c, len(ws), _stream()
+    )
+    _abi.check(rc, "lthc_read_multi_fwd")
+    return outs
+
+
+def weight_grad(high: torch.Tensor, lows) -> torch.Tensor:
+    b, h, _, c = high.shape
+    g = h // S
+    L = len(lows)
+    out = torch.empty((L, c, S * S), device=high.device, dtype=torch.float32)
+    nbytes = _abi.weight_grad_workspace_bytes(b, g, S, c, L)
+    ws = torch.empty((max(nbytes, 16),), device=high.device, dtype=torch.uint8)
+    rc = _lib().lthc_weight_grad(
+        high.data_ptr(), _abi.ptr_array(lows), _abi.code(high), out.data_ptr(), b, g, S, c, L, ws.data_ptr(), ws.numel(), _stream()
+    )
+    _abi.check(rc, "lthc_weight_grad")
+    return out
+
+
+def gamma(alpha: torch.Tensor, betas, out_dtype=torch.float32) -> torch.Tensor:
+    c, k = alpha.shape
+    out = torch.empty((len(betas), c), device=alpha.device, dtype=out_dtype)
+    rc = _lib().lthc_gamma(
+        alpha.data_ptr(), _abi.ptr_array(betas), _abi.code(alpha), out.data_ptr(), _abi.DTYPE_CODE[out_dtype], c, k, len(betas), _stream()
+    )
+    _abi.check(rc, "lthc_gamma")
+    return out
+
+
+def recur(z: torch.Tensor, dz: torch.Tensor, gam: torch.Tensor) -> torch.Tensor:
+    c = z.shape[-1]
+    out = torch.empty_like(z)
+    rc = _lib().lthc_recur_fwd(z.data_ptr(), dz.data_ptr(), _abi.code(z), gam.data_ptr(), _abi.code(gam), out.data_ptr(), z.numel() // c, c, _stream())
+    _abi.check(rc, "lthc_recur_fwd")
+    return out
+
+
+def recur_bwd(gr: torch.Tensor, dz: torch.Tensor, gam: torch.Tensor):
+    c = gr.shape[-1]
+    rows = gr.numel() // c
+    gdz = torch.empty_like(gr)
+    gg = torch.empty((c,), device=gr.device, dtype=torch.float32)
+    ws = torch.empty((max(_abi.recur_bwd_workspace_bytes(rows, c), 16),), device=gr.device, dtype=torch.uint8)
+    rc = _lib().lthc_recur_bwd(
+        gr.data_ptr(), dz.data_ptr(), _abi.code(gr), gam.data_ptr(), _abi.code(gam), gdz.data_ptr(), gg.data_ptr(), rows, c,
+        ws.data_ptr(), ws.numel(), _stream(),
+    )  # fmt: skip
+    _abi.check(rc, "lthc_recur_bwd")
+    return gdz, gg

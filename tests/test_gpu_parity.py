@@ -1,0 +1,305 @@
+"""GPU parity of the HIP kernels against the CPU oracle (MI355X only).
+
+Tolerances (north star): fp32 results must satisfy max|got - ref| / max|ref|
+<= 1e-5 per tensor (an elementwise relative bound is ill-conditioned where the
+reference crosses zero); bf16 results must satisfy max|got - ref| <= 2e-2
+against the oracle evaluated in fp64 on the same bf16-rounded inputs, and the
+tighter elementwise bound |got - ref| <= 2^-8 |ref| + 1e-5 (one
+round-to-nearest-even to bf16 after fp32 accumulation).
+Inputs come from oracle.make_inputs (seeded CPU torch.Generator), so the CPU
+and the GPU see identical bits.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from flowmatching_lthc_amd import ops
+from oracle import oracle as O
+
+from . import capi
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+F32, BF16 = torch.float32, torch.bfloat16
+
+
+def dev(a, dtype=F32):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV).to(dtype)
+
+
+def host(t: torch.Tensor) -> np.ndarray:
+    return t.detach().float().cpu().numpy()
+
+
+def rounded(a, dtype):
+    """The values the GPU sees after casting to `dtype`, as fp32 numpy."""
+    return host(dev(a, dtype))
+
+
+def assert_f32(got, ref, tol=1e-5, what=""):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    scale = max(np.abs(ref).max(), 1e-30)
+    err = np.abs(got - ref).max() / scale
+    assert err <= tol, f"{what}: max|d|/max|ref| = {err:.3e} > {tol}"
+
+
+def assert_bf16(got, ref, what=""):
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    d = np.abs(got - ref)
+    assert d.max() <= 2e-2, f"{what}: max abs err {d.max():.3e} > 2e-2"
+    bound = 2.0**-8 * np.abs(ref) + 1e-5
+    bad = int((d > bound).sum())
+    assert bad == 0, f"{what}: {bad} elements exceed 2^-8|ref| + 1e-5 (worst {np.max(d - bound):.3e})"
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _oracle_built(coracle):
+    coracle.set_threads(16)
+    yield
+
+
+def cfg(B, G, C, L, seed=0, grads=False):
+    return O.make_inputs(B, G, C, L, seed=seed, grads=grads)
+
+
+# ---------------------------------------------------------------------------
+# configuration 1: read + one write, fp32, B=2
+# ---------------------------------------------------------------------------
+def test_config1_read_and_write_fp32(coracle):
+    d = cfg(2, 16, 768, 1)
+    x0, alpha, beta, dz = d["x0"], d["alpha"], d["beta"][0], d["dz"][0]
+    z = capi.read(dev(x0), dev(alpha))
+    assert_f32(host(z), coracle.Cread(x0, alpha, 16), what="read")
+    xl = capi.materialise(dev(x0), [dev(dz)], [dev(beta)])
+    assert_f32(host(xl), coracle.Cwrite(x0, [dz], [beta]), what="write_add")
+    w = capi.materialise(None, [dev(dz)], [dev(beta)])
+    assert_f32(host(w), coracle.Cwrite(None, [dz], [beta], h=64), what="write")
+
+
+# ---------------------------------------------------------------------------
+# configuration 2: full lazy interface forward, bf16, B=32, L=12
+# ---------------------------------------------------------------------------
+def test_config2_lazy_interface_bf16(coracle):
+    B, G, C, L = 32, 16, 768, 12
+    d = cfg(B, G, C, L)
+    x0 = dev(d["x0"], BF16)
+    alpha = dev(d["alpha"])  # fp32 weights, as the released model passes them
+    betas = [dev(b) for b in d["beta"]]
+    dzs = [dev(z, BF16) for z in d["dz"]]
+    x0h, dzh = host(x0), [host(z) for z in dzs]
+
+    z = capi.read(x0, alpha)
+    assert_bf16(host(z), coracle.Cread(x0h, d["alpha"], G), what="read")
+
+    gam = capi.gamma(alpha, betas)
+    assert_f32(host(gam), coracle.Cgamma(d["alpha"], list(d["beta"])), tol=1e-6, what="gamma")
+
+    for l in range(L):  # each step against the oracle fed the same bf16 Z_l
+        zn = capi.recur(z, dzs[l], gam[l])
+        assert_bf16(host(zn), coracle.Crecur(host(z), dzh[l], host(gam[l])), what=f"recurrence step {l}")
+        z = zn
+
+    xl = capi.materialise(x0, dzs, betas)
+    assert_bf16(host(xl), coracle.Cwrite(x0h, dzh, list(d["beta"])), what="materialise")
+    xl_op = ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas)
+    assert torch.equal(xl_op, xl)
+
+
+# ---------------------------------------------------------------------------
+# configuration 3: forward + backward at training shape, bf16, B=64, L=12
+# ---------------------------------------------------------------------------
+def test_config3_materialise_backward_bf16(coracle):
+    B, G, C, L = 64, 16, 768, 12
+    d = cfg(B, G, C, L, grads=True)
+    gout = dev(d["grad_xl"], BF16)
+    dzs = [dev(z, BF16) for z in d["dz"]]
+    betas = [dev(b) for b in d["beta"]]
+    gh, dzh = host(gout), [host(z) for z in dzs]
+
+    gdz = ops.final_accumulate_b4_12_grad_dz_ptr_traceable(gout, *betas)
+    ref = coracle.Cread_multi(gh, list(d["beta"]), G)
+    for l in range(L):
+        assert_bf16(host(gdz[l]), ref[l], what=f"gdZ_{l}")
+
+    gb = ops.final_accumulate_b4_12_grad_beta_ptr_traceable(gout, *dzs)
+    gb_ref = coracle.Cweight_grad(gh, dzh, G)
+    assert gb.dtype == torch.float32
+    assert_f32(host(gb), gb_ref, tol=1e-5, what="gbeta")
+    gb2 = ops.final_accumulate_b4_12_grad_beta_ptr_traceable(gout, *dzs)
+    assert torch.equal(gb, gb2), "weight-gradient reduction is not deterministic"
+
+
+def test_config3_read_backward_bf16(coracle):
+    B, G, C = 64, 16, 768
+    d = cfg(B, G, C, 1, grads=True)
+    x0 = dev(d["x0"], BF16)
+    gz = dev(d["grad_z"][0], BF16)
+    alpha = dev(d["alpha"])
+    dx = capi.materialise(None, [gz], [alpha])
+    assert_bf16(host(dx), coracle.Cwrite(None, [host(gz)], [d["alpha"]], h=64), what="dX = R^T gZ")
+    da = capi.weight_grad(x0, [gz])[0]
+    assert_f32(host(da), coracle.Cweight_grad(host(x0), [host(gz)], G)[0], tol=1e-5, what="dalpha")
+
+
+def test_interface_autograd_matches_closed_form_fp32(coracle):
+    """Read op -> 4 recurrence ops -> stacked materialise op, backward through torch autograd."""
+    B, G, C, L = 2, 16, 64, 4
+    d = cfg(B, G, C, L, seed=3, grads=True)
+    t = lambda a: dev(a).requires_grad_(True)  # noqa: E731
+    x0, alpha = t(d["x0"]), t(d["alpha"])
+    betas, dzs = t(d["beta"]), [t(z) for z in d["dz"]]
+    z = ops.local_write_traceable(x0, alpha)
+    zs = [z]
+    for l in range(L):
+        gam = (alpha * betas[l]).sum(-1)
+        z = ops.lazy_workspace_update(z, dzs[l], gam)
+        zs.append(z)
+    xl = ops.final_accumulate_b4_traceable(x0, torch.stack(dzs), betas)
+    loss = (xl * dev(d["grad_xl"])).sum() + sum((zs[l] * dev(d["grad_z"][l])).sum() for l in range(L))
+    loss.backward()
+    ref = O.interface_bwd_np(d["x0"], d["alpha"], list(d["dz"]), list(d["beta"]), d["grad_xl"], list(d["grad_z"]), G)
+    assert_f32(host(x0.grad), ref["x0"], what="dX0")
+    assert_f32(host(alpha.grad), ref["alpha"], what="dalpha")
+    for l in range(L):
+        assert_f32(host(dzs[l].grad), ref["dz"][l], what=f"d dZ_{l}")
+        assert_f32(host(betas.grad[l]), ref["beta"][l], what=f"dbeta_{l}")
+
+
+def test_recurrence_backward(coracle):
+    d = cfg(8, 16, 768, 2, grads=True)
+    g, dz = dev(d["grad_z"][0], BF16), dev(d["dz"][0], BF16)
+    gam = dev(d["alpha"][:, 0] * 3.0)
+    gdz, gg = capi.recur_bwd(g, dz, gam)
+    rgdz, rgg = coracle.Crecur_bwd(host(g), host(dz), host(gam))
+    assert_bf16(host(gdz), rgdz, what="gamma * g")
+    assert_f32(host(gg), rgg, tol=1e-5, what="ggamma")
+
+
+# ---------------------------------------------------------------------------
+# configuration 5: 128x128 grid / 32x32 workspace, C=1024, L=24 (B=2 slice)
+# ---------------------------------------------------------------------------
+def test_config5_shape_bf16(coracle):
+    B, G, C, L = 2, 32, 1024, 24
+    d = cfg(B, G, C, L, grads=True)
+    x0, g = dev(d["x0"], BF16), dev(d["grad_xl"], BF16)
+    alpha, betas = dev(d["alpha"]), [dev(b) for b in d["beta"]]
+    dzs = [dev(z, BF16) for z in d["dz"]]
+    x0h, gh, dzh = host(x0), host(g), [host(z) for z in dzs]
+    assert_bf16(host(capi.read(x0, alpha)), coracle.Cread(x0h, d["alpha"], G), what="read")
+    assert_bf16(host(capi.materialise(x0, dzs, betas)), coracle.Cwrite(x0h, dzh, list(d["beta"])), what="materialise")
+    ref = coracle.Cread_multi(gh, list(d["beta"]), G)
+    for l, got in enumerate(capi.read_multi(g, betas)):
+        assert_bf16(host(got), ref[l], what=f"gdZ_{l}")
+    assert_f32(host(capi.weight_grad(g, dzs)), coracle.Cweight_grad(gh, dzh, G), what="gbeta")
+
+
+# ---------------------------------------------------------------------------
+# edge cases: ragged channel counts, every depth bucket, batch 1 and 0
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("B,G,C,L", [(1, 2, 4, 1), (3, 4, 260, 2), (1, 8, 12, 3), (2, 4, 36, 5), (1, 4, 20, 13), (1, 2, 8, 33), (1, 2, 8, 48)])
+def test_edge_shapes_fp32(coracle, B, G, C, L):
+    d = cfg(B, G, C, L, seed=B + G + C + L, grads=True)
+    x0, g = dev(d["x0"]), dev(d["grad_xl"])
+    betas, dzs = [dev(b) for b in d["beta"]], [dev(z) for z in d["dz"]]
+    assert_f32(host(capi.read(x0, dev(d["alpha"]))), coracle.Cread(d["x0"], d["alpha"], G), what="read")
+    assert_f32(host(capi.materialise(x0, dzs, betas)), coracle.Cwrite(d["x0"], list(d["dz"]), list(d["beta"])), what="materialise")
+    ref = coracle.Cread_multi(d["grad_xl"], list(d["beta"]), G)
+    for l, got in enumerate(capi.read_multi(g, betas)):
+        assert_f32(host(got), ref[l], what=f"gdZ_{l}")
+    assert_f32(host(capi.weight_grad(g, dzs)), coracle.Cweight_grad(d["grad_xl"], list(d["dz"]), G), what="gbeta")
+    gam = capi.gamma(dev(d["alpha"]), betas)
+    assert_f32(host(gam), coracle.Cgamma(d["alpha"], list(d["beta"])), tol=1e-6, what="gamma")
+
+
+def test_fp16_and_bf16_weights(coracle):
+    d = cfg(2, 16, 768, 3)
+    x0 = dev(d["x0"], torch.float16)
+    betas = [dev(b, BF16) for b in d["beta"]]
+    dzs = [dev(z, torch.float16) for z in d["dz"]]
+    got = host(capi.materialise(x0, dzs, betas))
+    ref = coracle.Cwrite(host(x0), [host(z) for z in dzs], [host(b) for b in betas])
+    d_ = np.abs(got - ref)
+    assert (d_ <= 2.0**-11 * np.abs(ref) + 1e-6).all(), f"fp16 rounding bound violated: {d_.max()}"
+
+
+def test_empty_batch_and_misaligned_inputs():
+    w = torch.full((8, 16), 1 / 16, device=DEV)
+    z = ops.local_write_traceable(torch.empty(0, 16, 16, 8, device=DEV), w)
+    assert z.shape == (0, 16, 8)
+    gw = ops.local_weight_grad_traceable(torch.empty(0, 16, 16, 8, device=DEV), torch.empty(0, 16, 8, device=DEV))
+    assert gw.shape == (8, 16) and float(gw.abs().max()) == 0.0
+    base = torch.randn(1 + 16 * 16 * 8, device=DEV)
+    x = base[1:].view(1, 16, 16, 8)  # storage offset of one element: misaligned for 16-byte vectors
+    ref = ops.local_write_traceable(x.clone(), w)
+    torch.testing.assert_close(ops.local_write_traceable(x, w), ref, rtol=0, atol=0)
+    with pytest.raises(ValueError, match="multiple of 4"):
+        ops.local_write_traceable(torch.randn(1, 16, 16, 6, device=DEV), torch.ones(6, 16, device=DEV))
+    with pytest.raises(ValueError, match="cell side"):
+        ops.local_write_traceable(torch.randn(1, 18, 18, 8, device=DEV), w)
+
+
+# ---------------------------------------------------------------------------
+# metric shape (B=256, C=768, L=12): size-independent properties
+# ---------------------------------------------------------------------------
+def test_metric_shape_properties_bf16():
+    B, G, C, L = 256, 16, 768, 12
+    gen = torch.Generator(device=DEV).manual_seed(0)
+    x0 = torch.randn((B, 64, 64, C), generator=gen, device=DEV).to(BF16)
+    alpha = torch.randn((C, 16), generator=gen, device=DEV) * 0.01 + 1 / 16
+    betas = [torch.randn((C, 16), generator=gen, device=DEV) * 0.02 for _ in range(L)]
+    dzs = [(torch.randn((B, 256, C), generator=gen, device=DEV) * 0.02).to(BF16) for _ in range(L)]
+    # dZ == 0 leaves X0 bit-for-bit unchanged
+    zeros = [torch.zeros_like(dzs[0])] * L
+    assert torch.equal(capi.materialise(x0, zeros, betas), x0)
+    # lazy invariant: read(X_L) == Z_L from the recurrence (bf16 rounding on both sides)
+    xl = capi.materialise(x0, dzs, betas)
+    z = capi.read(x0, alpha)
+    gam = capi.gamma(alpha, betas)
+    for l in range(L):
+        z = capi.recur(z, dzs[l], gam[l])
+    diff = (capi.read(xl, alpha).float() - z.float()).abs().max().item()
+    assert diff <= 2e-2, f"R(X_L) vs Z_L: {diff}"
+    # adjoint identity <R X, Zg> == <X, R^T Zg> in fp64 accumulation of fp32 kernel outputs
+    xf = x0[:32].float()
+    zg = dzs[0][:32].float()
+    lhs = (capi.read(xf, alpha).double() * zg.double()).sum().item()
+    rhs = (xf.double() * capi.materialise(None, [zg], [alpha]).double()).sum().item()
+    assert abs(lhs - rhs) <= 1e-5 * max(1.0, abs(lhs))
+    # checksum of checksums: sum_k gbeta_l[c,k] == sum_{b,m} dZ_l * read_{w=1}(G)
+    gb = capi.weight_grad(x0, dzs[:2])
+    ones = torch.ones((C, 16), device=DEV)
+    r1 = capi.read(x0.float(), ones).double()
+    for l in range(2):
+        lhs = gb[l].double().sum(-1)
+        rhs = (r1 * dzs[l].double()).sum((0, 1))
+        assert ((lhs - rhs).abs().max() / rhs.abs().max()).item() <= 1e-5
+
+
+def test_hip_graph_replay_matches_eager():
+    B, G, C, L = 4, 16, 768, 12
+    gen = torch.Generator(device=DEV).manual_seed(1)
+    x0 = torch.randn((B, 64, 64, C), generator=gen, device=DEV).to(BF16)
+    betas = [torch.randn((C, 16), generator=gen, device=DEV) * 0.02 for _ in range(L)]
+    dzs = [(torch.randn((B, 256, C), generator=gen, device=DEV) * 0.02).to(BF16) for _ in range(L)]
+    eager = ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas)
+    gb_eager = ops.final_accumulate_b4_12_grad_beta_ptr_traceable(x0, *dzs)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas)  # warm the allocator on this stream
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas)
+        gb = ops.final_accumulate_b4_12_grad_beta_ptr_traceable(x0, *dzs)
+    for i in range(3):
+        out.zero_()
+        gb.zero_()
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        assert torch.equal(gb, gb_eager), f"replay {i}"
