@@ -48,6 +48,12 @@ def parse_args():
     p.add_argument("--mode", choices=["graph", "eager"], default="graph", help="how `value` is timed")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument(
+        "--profile",
+        choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy"],
+        help="run only this kernel --steps times at the configured shape (for rocprofv3), plus one plain copy "
+        "of X0 (a copy kernel of known size that calibrates the FETCH_SIZE / WRITE_SIZE counters)",
+    )
     return p.parse_args()
 
 
@@ -117,6 +123,30 @@ def cpu_baseline(G, C, L, budget_s):
     }
 
 
+def profile(args, ops, inputs, alpha, beta_stack, betas):
+    """One kernel, --warmup + --steps launches, then a plain copy of X0 (bytes known: 2 x X0)."""
+    import torch
+
+    x0, dzs = inputs
+    z = ops.local_write_traceable(x0, alpha)
+    gam = ops.lazy_gamma_stack(alpha, beta_stack)
+    run = {
+        "materialise": lambda: ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas),
+        "read": lambda: ops.local_write_traceable(x0, alpha),
+        "recur": lambda: ops.lazy_workspace_update(z, dzs[0], gam[0]),
+        "read_multi": lambda: ops.final_accumulate_b4_12_grad_dz_ptr_traceable(x0, *betas),
+        "weight_grad": lambda: ops.final_accumulate_b4_12_grad_beta_ptr_traceable(x0, *dzs),
+        "copy": lambda: None,
+    }[args.profile]
+    for _ in range(args.warmup + args.steps):
+        run()
+    torch.cuda.synchronize()
+    y = torch.empty_like(x0)
+    y.copy_(x0)
+    torch.cuda.synchronize()
+    print(f"profiled {args.profile} x{args.warmup + args.steps}; calibration copy of {x0.numel() * x0.element_size()} bytes")
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -172,6 +202,10 @@ def main():
             e1.record(stream)
             mat_events.append((e0, e1))
         return z, xl
+
+    if args.profile:
+        profile(args, ops, sets[0], alpha, beta_stack, betas)
+        return
 
     # eager: warmup, then K timed steps with events around every materialise launch
     for i in range(args.warmup):

@@ -9,18 +9,23 @@
 // tensors are [B, G*G, C].  Weights are [C, 16] (tap index fastest).
 //
 // Every kernel here is HBM-bandwidth bound: 1 to 24 fp32 FMAs per element
-// moved.  Lanes of a wavefront always run along the channel axis so that a
-// wavefront load covers one contiguous 512 B .. 1 KiB span of a tap; the
-// per-channel weights a thread needs are loaded into VGPRs once per block
-// and reused for every cell the block visits.
+// moved.  Lanes of a wavefront run along the channel axis, so one wavefront
+// load covers a contiguous 512 B .. 1 KiB run of one tap.  The per-channel
+// weights a thread needs are loaded into VGPRs once per block and reused for
+// every cell the block visits.  Each cell iteration is written as two phases
+// separated by a scheduling barrier: (1) issue every vector load of the cell,
+// (2) widen, FMA, narrow and store.  Loads are never placed under a
+// data-dependent branch (padding layers read a valid clamped pointer and are
+// masked by a select), so a wavefront keeps all of a cell's loads in flight
+// instead of waiting on each one.
 
 #include <hip/hip_runtime.h>
 
 #include <stdint.h>
 
 #include <algorithm>
-#include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "../../include/lthc.h"
 
@@ -37,104 +42,156 @@ constexpr int kBlock = 256;  // threads per block of the cell kernels
 // ---------------------------------------------------------------------------
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 template <int DT>
-struct Fmt;
-template <>
-struct Fmt<LTHC_F32> {
-  static constexpr int bytes = 4;
-};
-template <>
-struct Fmt<LTHC_BF16> {
-  static constexpr int bytes = 2;
-};
-template <>
-struct Fmt<LTHC_F16> {
-  static constexpr int bytes = 2;
+struct Fmt {
+  static constexpr int bytes = DT == LTHC_F32 ? 4 : 2;
 };
 
 template <int DT>
-LTHC_DEV void unpack2(uint32_t w, float& a, float& b);
-template <>
-LTHC_DEV void unpack2<LTHC_BF16>(uint32_t w, float& a, float& b) {
-  a = __uint_as_float(w << 16);
-  b = __uint_as_float(w & 0xffff0000u);
+LTHC_DEV float widen1(uint32_t h16) {
+  if constexpr (DT == LTHC_BF16) return __uint_as_float(h16 << 16);
+  else return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h16)));
 }
-template <>
-LTHC_DEV void unpack2<LTHC_F16>(uint32_t w, float& a, float& b) {
-  const f16x2_t h = __builtin_bit_cast(f16x2_t, w);
-  a = static_cast<float>(h.x);
-  b = static_cast<float>(h.y);
+
+template <int DT>
+LTHC_DEV void unpack2(uint32_t w, float& a, float& b) {
+  if constexpr (DT == LTHC_BF16) {
+    a = __uint_as_float(w << 16);
+    b = __uint_as_float(w & 0xffff0000u);
+  } else {
+    const f16x2_t h = __builtin_bit_cast(f16x2_t, w);
+    a = static_cast<float>(h.x);
+    b = static_cast<float>(h.y);
+  }
 }
 
 // Round-to-nearest-even narrowing (v_cvt_pk_bf16_f32 / v_cvt_f16_f32).
 template <int DT>
-LTHC_DEV uint32_t pack2(float a, float b);
-template <>
-LTHC_DEV uint32_t pack2<LTHC_BF16>(float a, float b) {
-  const bf16x2_t r = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
-  return __builtin_bit_cast(uint32_t, r);
-}
-template <>
-LTHC_DEV uint32_t pack2<LTHC_F16>(float a, float b) {
-  const f16x2_t r = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
-  return __builtin_bit_cast(uint32_t, r);
+LTHC_DEV uint32_t pack2(float a, float b) {
+  if constexpr (DT == LTHC_BF16) {
+    const bf16x2_t r = {static_cast<__bf16>(a), static_cast<__bf16>(b)};
+    return __builtin_bit_cast(uint32_t, r);
+  } else {
+    const f16x2_t r = {static_cast<_Float16>(a), static_cast<_Float16>(b)};
+    return __builtin_bit_cast(uint32_t, r);
+  }
 }
 
-// N consecutive elements starting at element index i, widened to fp32.
+// Raw storage of N consecutive elements of format DT (N * bytes >= 4).
+template <int DT, int N>
+struct Raw {
+  static constexpr int kWords = N * Fmt<DT>::bytes / 4;
+  static_assert(kWords >= 1 && (kWords <= 2 || kWords % 4 == 0), "raw vector width");
+  uint32_t w[kWords];
+};
+
+// One vector load (dwordx1/x2/x4, several x4 for wider runs) of the raw
+// bytes at base + boff; NT = streaming (non-temporal).  With a uniform base
+// and a 32-bit offset (Off = uint32_t) this is the saddr + voffset form, so
+// the per-lane address costs one VGPR and no 64-bit arithmetic.
+template <int DT, int N, bool NT = false, typename Off = int64_t>
+LTHC_DEV void load_at(const void* __restrict__ base, Off boff, Raw<DT, N>& r) {
+  constexpr int W = Raw<DT, N>::kWords;
+  const char* q = static_cast<const char*>(base) + boff;
+  if constexpr (W == 1) {
+    r.w[0] = NT ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(q)) : *reinterpret_cast<const uint32_t*>(q);
+  } else if constexpr (W == 2) {
+    const u32x2_t t = NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(q)) : *reinterpret_cast<const u32x2_t*>(q);
+    r.w[0] = t.x;
+    r.w[1] = t.y;
+  } else {
+#pragma unroll
+    for (int j = 0; j < W / 4; ++j) {
+      const u32x4_t* v = reinterpret_cast<const u32x4_t*>(q) + j;
+      const u32x4_t t = NT ? __builtin_nontemporal_load(v) : *v;
+      r.w[4 * j + 0] = t.x;
+      r.w[4 * j + 1] = t.y;
+      r.w[4 * j + 2] = t.z;
+      r.w[4 * j + 3] = t.w;
+    }
+  }
+}
+
+// Element-index form.
+template <int DT, int N, bool NT = false>
+LTHC_DEV void load_raw(const void* __restrict__ p, int64_t i, Raw<DT, N>& r) {
+  load_at<DT, N, NT>(p, i * Fmt<DT>::bytes, r);
+}
+
+template <int DT, int N>
+LTHC_DEV void unpack_raw(const Raw<DT, N>& r, float (&v)[N]) {
+  if constexpr (DT == LTHC_F32) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = __uint_as_float(r.w[j]);
+  } else {
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) unpack2<DT>(r.w[j], v[2 * j], v[2 * j + 1]);
+  }
+}
+
 template <int DT, int N>
 LTHC_DEV void load_vec(const void* __restrict__ p, int64_t i, float (&v)[N]) {
-  static_assert(N == 4 || N == 8, "vector width");
+  Raw<DT, N> r;
+  load_raw<DT, N>(p, i, r);
+  unpack_raw<DT, N>(r, v);
+}
+
+template <int DT, int N, bool NT = false, typename Off = int64_t>
+LTHC_DEV void store_at(void* __restrict__ base, Off boff, const float (&v)[N]) {
+  constexpr int W = N * Fmt<DT>::bytes / 4;
+  uint32_t w[W];
   if constexpr (DT == LTHC_F32) {
-    const float4* q = reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
 #pragma unroll
-    for (int j = 0; j < N / 4; ++j) {
-      const float4 r = q[j];
-      v[4 * j + 0] = r.x;
-      v[4 * j + 1] = r.y;
-      v[4 * j + 2] = r.z;
-      v[4 * j + 3] = r.w;
-    }
+    for (int j = 0; j < N; ++j) w[j] = __float_as_uint(v[j]);
   } else {
-    const uint16_t* q = static_cast<const uint16_t*>(p) + i;
-    if constexpr (N == 4) {
-      const uint2 r = *reinterpret_cast<const uint2*>(q);
-      unpack2<DT>(r.x, v[0], v[1]);
-      unpack2<DT>(r.y, v[2], v[3]);
-    } else {
-      const uint4 r = *reinterpret_cast<const uint4*>(q);
-      unpack2<DT>(r.x, v[0], v[1]);
-      unpack2<DT>(r.y, v[2], v[3]);
-      unpack2<DT>(r.z, v[4], v[5]);
-      unpack2<DT>(r.w, v[6], v[7]);
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) w[j] = pack2<DT>(v[2 * j], v[2 * j + 1]);
+  }
+  char* q = static_cast<char*>(base) + boff;
+  if constexpr (W == 1) {
+    if (NT) __builtin_nontemporal_store(w[0], reinterpret_cast<uint32_t*>(q));
+    else *reinterpret_cast<uint32_t*>(q) = w[0];
+  } else if constexpr (W == 2) {
+    const u32x2_t t = {w[0], w[1]};
+    if (NT) __builtin_nontemporal_store(t, reinterpret_cast<u32x2_t*>(q));
+    else *reinterpret_cast<u32x2_t*>(q) = t;
+  } else {
+    static_assert(W % 4 == 0, "store width");
+#pragma unroll
+    for (int j = 0; j < W / 4; ++j) {
+      const u32x4_t t = {w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
+      if (NT) __builtin_nontemporal_store(t, reinterpret_cast<u32x4_t*>(q) + j);
+      else reinterpret_cast<u32x4_t*>(q)[j] = t;
     }
   }
 }
 
-template <int DT, int N>
+template <int DT, int N, bool NT = false>
 LTHC_DEV void store_vec(void* __restrict__ p, int64_t i, const float (&v)[N]) {
-  static_assert(N == 4 || N == 8, "vector width");
-  if constexpr (DT == LTHC_F32) {
-    float4* q = reinterpret_cast<float4*>(static_cast<float*>(p) + i);
-#pragma unroll
-    for (int j = 0; j < N / 4; ++j) q[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+  store_at<DT, N, NT>(p, i * Fmt<DT>::bytes, v);
+}
+
+// N consecutive weights of format WDT, widened to fp32 (one vector load
+// where the width allows it).
+template <int WDT, int N>
+LTHC_DEV void load_wvec(const void* __restrict__ p, int64_t i, float (&v)[N]) {
+  if constexpr (WDT == LTHC_F32 || N % 2 == 0) {
+    load_vec<WDT, N>(p, i, v);
   } else {
-    uint16_t* q = static_cast<uint16_t*>(p) + i;
-    if constexpr (N == 4) {
-      *reinterpret_cast<uint2*>(q) = make_uint2(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]));
-    } else {
-      *reinterpret_cast<uint4*>(q) = make_uint4(pack2<DT>(v[0], v[1]), pack2<DT>(v[2], v[3]),
-                                                pack2<DT>(v[4], v[5]), pack2<DT>(v[6], v[7]));
-    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) v[j] = widen1<WDT>(static_cast<const uint16_t*>(p)[i + j]);
   }
 }
 
-// One weight element of a runtime dtype, widened to fp32.
+// Scalar weight of a runtime dtype (small kernels only).
 LTHC_DEV float load_w(const void* __restrict__ p, int dt, int64_t i) {
   if (dt == LTHC_F32) return static_cast<const float*>(p)[i];
   const uint16_t h = static_cast<const uint16_t*>(p)[i];
-  if (dt == LTHC_BF16) return __uint_as_float(static_cast<uint32_t>(h) << 16);
-  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+  if (dt == LTHC_BF16) return widen1<LTHC_BF16>(h);
+  return widen1<LTHC_F16>(h);
 }
 
 LTHC_DEV void store_w(void* __restrict__ p, int dt, int64_t i, float v) {
@@ -151,126 +208,187 @@ struct PtrPack {
   const void* p[LTHC_MAX_LAYERS];
 };
 
-// Offset of tap (sy, sx0) of cell `cell` at channel c0 in an NHWC tensor.
-LTHC_DEV int64_t tap_offset(int64_t cell, int G, int C, int sy, int sx0, int c0) {
-  const int M = G * G;
-  const int H = G * kS;
-  const int64_t b = cell / M;
-  const int m = static_cast<int>(cell - b * M);
-  const int gy = m / G;
-  const int gx = m - gy * G;
-  return ((b * H + gy * kS + sy) * H + gx * kS + sx0) * static_cast<int64_t>(C) + c0;
-}
+// Walks consecutive cells without divisions.  hoff = element offset of tap
+// (0, 0), channel 0 of the current cell in the NHWC tensor; zoff = cell * C.
+// Stepping to the next cell adds 4C to hoff, plus 3 high-res rows (3HC) when
+// the cell row wraps (the next cell row starts 4 high-res rows down; the
+// batch boundary needs no extra term because H = 4G).
+struct CellWalk {
+  int64_t hoff;
+  int64_t zoff;
+  int gx;
+
+  LTHC_DEV void init(int64_t cell, int G, int C) {
+    const int M = G * G;
+    const int64_t H = static_cast<int64_t>(G) * kS;
+    const int64_t b = cell / M;
+    const int m = static_cast<int>(cell - b * M);
+    const int gy = m / G;
+    gx = m - gy * G;
+    hoff = ((b * H + gy * kS) * H + gx * kS) * C;
+    zoff = cell * C;
+  }
+  LTHC_DEV void next(int G, int C, int64_t row_skip) {
+    zoff += C;
+    hoff += kS * C;
+    if (++gx == G) {
+      gx = 0;
+      hoff += row_skip;
+    }
+  }
+};
+
+#define LTHC_PHASE_BARRIER() __builtin_amdgcn_sched_barrier(0)
 
 // ---------------------------------------------------------------------------
 // READ: z[cell, c] = sum_k alpha[c,k] x[cell, k, c]
 // Thread = VEC channels of one cell, all 16 taps; alpha for those channels
-// lives in VGPRs.  Block = cpi cells x ncv_blk channel vectors.
+// lives in VGPRs.  Block = cpi cells x ncv_blk channel vectors; each thread
+// walks every cpi-th cell of the block's range.  Off is the byte-offset type
+// (uint32_t when x is smaller than 4 GiB).
+// Accumulation order k = 0..15 (local_thc_triton_kernels.py:51-55).
 // ---------------------------------------------------------------------------
-template <int DT, int VEC>
+template <int DT, int WDT, int VEC, typename Off>
 __global__ __launch_bounds__(kBlock) void read_fwd_kernel(const void* __restrict__ x, const void* __restrict__ w,
-                                                          int wdt, void* __restrict__ z, int64_t ncells, int G,
-                                                          int C, int ncv_blk, int cpi, int64_t cpb) {
+                                                          void* __restrict__ z, int64_t ncells, int G, int C,
+                                                          int ncv_blk, int cpi, int64_t cpb) {
+  constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int ci = t / ncv_blk;
   const int c0 = (blockIdx.y * ncv_blk + (t - ci * ncv_blk)) * VEC;
   if (ci >= cpi || c0 >= C) return;
-  float a[kK][VEC];
+  float a[VEC][kK];
 #pragma unroll
-  for (int k = 0; k < kK; ++k)
-#pragma unroll
-    for (int v = 0; v < VEC; ++v) a[k][v] = load_w(w, wdt, static_cast<int64_t>(c0 + v) * kK + k);
+  for (int v = 0; v < VEC; ++v) load_wvec<WDT, kK>(w, static_cast<int64_t>(c0 + v) * kK, a[v]);
 
-  const int64_t row = static_cast<int64_t>(G) * kS * C;  // one high-res row
+  const Off row_b = static_cast<Off>(static_cast<int64_t>(G) * kS * C * ES);  // one high-res row, bytes
+  const Off tap_b = static_cast<Off>(C * ES);
+  const int64_t row_skip = 3 * static_cast<int64_t>(G) * kS * C;
   const int64_t cb = static_cast<int64_t>(blockIdx.x) * cpb;
   const int64_t ce = std::min(ncells, cb + cpb);
+  CellWalk cw;
+  cw.init(cb + ci, G, C);
   for (int64_t cell = cb + ci; cell < ce; cell += cpi) {
-    const int64_t o = tap_offset(cell, G, C, 0, 0, c0);
+    const Off xo = static_cast<Off>((cw.hoff + c0) * ES);
+    Raw<DT, VEC> xr[kK];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) load_at<DT, VEC, true>(x, xo + (k / kS) * row_b + (k % kS) * tap_b, xr[k]);
+    const Off zo = static_cast<Off>((cw.zoff + c0) * ES);
+    for (int i = 0; i < cpi; ++i) cw.next(G, C, row_skip);
+    LTHC_PHASE_BARRIER();
     float acc[VEC];
 #pragma unroll
     for (int v = 0; v < VEC; ++v) acc[v] = 0.f;
 #pragma unroll
     for (int k = 0; k < kK; ++k) {
       float xv[VEC];
-      load_vec<DT, VEC>(x, o + (k / kS) * row + (k % kS) * C, xv);
+      unpack_raw<DT, VEC>(xr[k], xv);
 #pragma unroll
-      for (int v = 0; v < VEC; ++v) acc[v] = fmaf(xv[v], a[k][v], acc[v]);
+      for (int v = 0; v < VEC; ++v) acc[v] = fmaf(xv[v], a[v][k], acc[v]);
     }
-    store_vec<DT, VEC>(z, cell * C + c0, acc);
+    store_at<DT, VEC>(z, zo, acc);
   }
 }
 
 // ---------------------------------------------------------------------------
 // MATERIALISE / WRITE: out[cell,k,c] = base[cell,k,c] + sum_l beta_l[c,k] dz_l[cell,c]
-// Thread = 4 channels x TPT taps of one tap row; its LMAX x TPT x 4 write
-// weights stay in VGPRs.  Block = 256 threads = QS channel quads x NTG tap
-// groups covering all 16 taps of a 4*QS channel slab; the block walks cpb
-// consecutive cells.  dz_l is loaded by each of the NTG tap-group threads
-// of a quad (served by L1 after the first).
+// Thread = CPT channels x TPT taps of one tap row; its LMAX x CPT x TPT write
+// weights stay in VGPRs.  Block = 256 threads = QS channel groups x NTG tap
+// groups, covering all 16 taps of a CPT*QS channel slab; the block walks cpb
+// consecutive cells, the cell position being uniform (scalar) across the
+// block.  The NTG tap-group threads of a channel group load the same dz runs
+// (L1 hits after the first).  When L < LMAX (EXACT == false) the padding
+// layers load layer 0 and contribute a selected 0.
+// Accumulation: acc = base, acc = fma(beta_l, dz_l, acc) for l = 0..L-1
+// (local_thc_triton_kernels.py:367-403).  NT marks the base reads and the
+// output writes as streaming, keeping L2 for the dz runs.
 // ---------------------------------------------------------------------------
-template <int DT, int LMAX, int TPT>
+template <int DT, int WDT, int LMAX, int TPT, int CPT, bool HAS_BASE, bool EXACT, bool NT, typename Off>
 __global__ __launch_bounds__(kBlock) void materialise_kernel(const void* __restrict__ base, PtrPack dz, PtrPack beta,
-                                                             int wdt, void* __restrict__ out, int L, int64_t ncells,
-                                                             int G, int C, int64_t cpb) {
+                                                             void* __restrict__ out, int L, int64_t ncells, int G,
+                                                             int C, int64_t cpb) {
   constexpr int NTG = kK / TPT;
   constexpr int QS = kBlock / NTG;
+  constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int g = t / QS;
-  const int c0 = (blockIdx.y * QS + (t - g * QS)) * 4;
+  const int c0 = (blockIdx.y * QS + (t - g * QS)) * CPT;
   if (c0 >= C) return;
   const int tap0 = g * TPT;
   const int sy = tap0 / kS;
   const int sx0 = tap0 % kS;
 
-  float bw[LMAX][TPT][4];
+  float bw[LMAX][CPT][TPT];
 #pragma unroll
-  for (int l = 0; l < LMAX; ++l)
+  for (int l = 0; l < LMAX; ++l) {
+    const void* bp = beta.p[(EXACT || l < L) ? l : 0];
 #pragma unroll
-    for (int j = 0; j < TPT; ++j)
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        bw[l][j][v] = (l < L) ? load_w(beta.p[l], wdt, static_cast<int64_t>(c0 + v) * kK + tap0 + j) : 0.f;
+    for (int v = 0; v < CPT; ++v) load_wvec<WDT, TPT>(bp, static_cast<int64_t>(c0 + v) * kK + tap0, bw[l][v]);
+  }
 
+  const int64_t H = static_cast<int64_t>(G) * kS;
+  const Off lane_h = static_cast<Off>(((sy * H + sx0) * C + c0) * ES);
+  const Off lane_z = static_cast<Off>(c0 * ES);
+  const Off tap_b = static_cast<Off>(C * ES);
+  const int64_t row_skip = 3 * H * C;
   const int64_t cb = static_cast<int64_t>(blockIdx.x) * cpb;
   const int64_t ce = std::min(ncells, cb + cpb);
+  CellWalk cw;
+  cw.init(cb, G, C);
   for (int64_t cell = cb; cell < ce; ++cell) {
-    const int64_t o = tap_offset(cell, G, C, sy, sx0, c0);
-    float acc[TPT][4];
-    if (base != nullptr) {
+    const Off xo = static_cast<Off>(cw.hoff * ES) + lane_h;
+    const Off zo = static_cast<Off>(cw.zoff * ES) + lane_z;
+    cw.next(G, C, row_skip);
+    Raw<DT, CPT> xr[TPT];
+    Raw<DT, CPT> dr[LMAX];
+    if constexpr (HAS_BASE) {
 #pragma unroll
-      for (int j = 0; j < TPT; ++j) load_vec<DT, 4>(base, o + j * C, acc[j]);
-    } else {
-#pragma unroll
-      for (int j = 0; j < TPT; ++j)
-#pragma unroll
-        for (int v = 0; v < 4; ++v) acc[j][v] = 0.f;
+      for (int j = 0; j < TPT; ++j) load_at<DT, CPT, NT>(base, xo + j * tap_b, xr[j]);
     }
-    const int64_t zo = cell * C + c0;
 #pragma unroll
-    for (int l = 0; l < LMAX; ++l) {
-      if (l < L) {
-        float d[4];
-        load_vec<DT, 4>(dz.p[l], zo, d);
+    for (int l = 0; l < LMAX; ++l) load_at<DT, CPT>(dz.p[(EXACT || l < L) ? l : 0], zo, dr[l]);
+    LTHC_PHASE_BARRIER();
+
+    float acc[TPT][CPT];
 #pragma unroll
-        for (int j = 0; j < TPT; ++j)
+    for (int j = 0; j < TPT; ++j) {
+      if constexpr (HAS_BASE) {
+        unpack_raw<DT, CPT>(xr[j], acc[j]);
+      } else {
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[j][v] = fmaf(bw[l][j][v], d[v], acc[j][v]);
+        for (int v = 0; v < CPT; ++v) acc[j][v] = 0.f;
       }
     }
 #pragma unroll
-    for (int j = 0; j < TPT; ++j) store_vec<DT, 4>(out, o + j * C, acc[j]);
+    for (int l = 0; l < LMAX; ++l) {
+      float d[CPT];
+      unpack_raw<DT, CPT>(dr[l], d);
+      if constexpr (!EXACT) {
+        const bool live = l < L;
+#pragma unroll
+        for (int v = 0; v < CPT; ++v) d[v] = live ? d[v] : 0.f;
+      }
+#pragma unroll
+      for (int j = 0; j < TPT; ++j)
+#pragma unroll
+        for (int v = 0; v < CPT; ++v) acc[j][v] = fmaf(bw[l][v][j], d[v], acc[j][v]);
+    }
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) store_at<DT, CPT, NT>(out, xo + j * tap_b, acc[j]);
   }
 }
 
 // ---------------------------------------------------------------------------
 // MULTI-WEIGHT READ: out_l[cell,c] = sum_k w_l[c,k] g[cell,k,c]
-// Thread = 4 channels x 16 taps x LC layers; the LC x 16 x 4 weights stay in
+// Thread = 4 channels x 16 taps x LC layers; the LC x 4 x 16 weights stay in
 // VGPRs.  Block = QS quads x NLG layer groups (at most 256 threads); the NLG
 // groups of a quad read the same g run (L1 hits after the first).
+// Accumulation order k = 0..15 (local_thc_triton_kernels.py:580-592).
 // ---------------------------------------------------------------------------
-template <int DT, int LC>
-__global__ __launch_bounds__(kBlock) void read_multi_kernel(const void* __restrict__ g, PtrPack w, int wdt, PtrPack out,
-                                                          int L, int QS, int64_t ncells, int G, int C, int64_t cpb) {
+template <int DT, int WDT, int LC, typename Off>
+__global__ __launch_bounds__(kBlock) void read_multi_kernel(const void* __restrict__ g, PtrPack w, PtrPack out, int L,
+                                                            int QS, int64_t ncells, int G, int C, int64_t cpb) {
+  constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int lg = t / QS;
   const int c0 = (blockIdx.y * QS + (t - lg * QS)) * 4;
@@ -278,20 +396,31 @@ __global__ __launch_bounds__(kBlock) void read_multi_kernel(const void* __restri
   if (c0 >= C || l0 >= L) return;
   const int nl = std::min(LC, L - l0);
 
-  float wr[LC][kK][4];
+  float wr[LC][4][kK];
 #pragma unroll
-  for (int i = 0; i < LC; ++i)
+  for (int i = 0; i < LC; ++i) {
+    const void* wp = w.p[l0 + (i < nl ? i : 0)];
 #pragma unroll
-    for (int k = 0; k < kK; ++k)
-#pragma unroll
-      for (int v = 0; v < 4; ++v)
-        wr[i][k][v] = (i < nl) ? load_w(w.p[l0 + i], wdt, static_cast<int64_t>(c0 + v) * kK + k) : 0.f;
+    for (int v = 0; v < 4; ++v) load_wvec<WDT, kK>(wp, static_cast<int64_t>(c0 + v) * kK, wr[i][v]);
+  }
 
-  const int64_t row = static_cast<int64_t>(G) * kS * C;
+  const int64_t H = static_cast<int64_t>(G) * kS;
+  const Off row_b = static_cast<Off>(H * C * ES);
+  const Off tap_b = static_cast<Off>(C * ES);
+  const Off lane_c = static_cast<Off>(c0 * ES);
+  const int64_t row_skip = 3 * H * C;
   const int64_t cb = static_cast<int64_t>(blockIdx.x) * cpb;
   const int64_t ce = std::min(ncells, cb + cpb);
+  CellWalk cw;
+  cw.init(cb, G, C);
   for (int64_t cell = cb; cell < ce; ++cell) {
-    const int64_t o = tap_offset(cell, G, C, 0, 0, c0);
+    const Off go = static_cast<Off>(cw.hoff * ES) + lane_c;
+    const Off zo = static_cast<Off>(cw.zoff * ES) + lane_c;
+    cw.next(G, C, row_skip);
+    Raw<DT, 4> gr[kK];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) load_at<DT, 4>(g, go + (k / kS) * row_b + (k % kS) * tap_b, gr[k]);
+    LTHC_PHASE_BARRIER();
     float acc[LC][4];
 #pragma unroll
     for (int i = 0; i < LC; ++i)
@@ -300,64 +429,79 @@ __global__ __launch_bounds__(kBlock) void read_multi_kernel(const void* __restri
 #pragma unroll
     for (int k = 0; k < kK; ++k) {
       float gv[4];
-      load_vec<DT, 4>(g, o + (k / kS) * row + (k % kS) * C, gv);
+      unpack_raw<DT, 4>(gr[k], gv);
 #pragma unroll
       for (int i = 0; i < LC; ++i)
 #pragma unroll
-        for (int v = 0; v < 4; ++v) acc[i][v] = fmaf(gv[v], wr[i][k][v], acc[i][v]);
+        for (int v = 0; v < 4; ++v) acc[i][v] = fmaf(gv[v], wr[i][v][k], acc[i][v]);
     }
 #pragma unroll
     for (int i = 0; i < LC; ++i)
-      if (i < nl) store_vec<DT, 4>(const_cast<void*>(out.p[l0 + i]), cell * C + c0, acc[i]);
+      if (i < nl) store_at<DT, 4>(const_cast<void*>(out.p[l0 + i]), zo, acc[i]);
   }
 }
 
 // ---------------------------------------------------------------------------
 // CELL WEIGHT GRADIENT, stage 1: per-block partial sums
 //   partial[bx, l, c, k] = sum_{cells of block bx} high[cell,k,c] low_l[cell,c]
-// Same thread mapping as materialise_kernel; the LMAX x TPT x 4 accumulators
-// stay in VGPRs for the whole cell range of the block.
+// Same thread mapping as materialise_kernel; the LMAX x TPT x CPT
+// accumulators stay in VGPRs for the whole cell range of the block.  Padding
+// layers (l >= L) accumulate layer 0 and are never written out.
 // ---------------------------------------------------------------------------
-template <int DT, int LMAX, int TPT>
+template <int DT, int LMAX, int TPT, int CPT, bool NT, typename Off>
 __global__ __launch_bounds__(kBlock) void wgrad_partial_kernel(const void* __restrict__ high, PtrPack low,
                                                                float* __restrict__ partial, int L, int64_t ncells,
                                                                int G, int C, int64_t cpb) {
   constexpr int NTG = kK / TPT;
   constexpr int QS = kBlock / NTG;
+  constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int g = t / QS;
-  const int c0 = (blockIdx.y * QS + (t - g * QS)) * 4;
+  const int c0 = (blockIdx.y * QS + (t - g * QS)) * CPT;
   if (c0 >= C) return;
   const int tap0 = g * TPT;
   const int sy = tap0 / kS;
   const int sx0 = tap0 % kS;
 
-  float acc[LMAX][TPT][4];
+  float acc[LMAX][TPT][CPT];
 #pragma unroll
   for (int l = 0; l < LMAX; ++l)
 #pragma unroll
     for (int j = 0; j < TPT; ++j)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[l][j][v] = 0.f;
+      for (int v = 0; v < CPT; ++v) acc[l][j][v] = 0.f;
 
+  const int64_t H = static_cast<int64_t>(G) * kS;
+  const Off lane_h = static_cast<Off>(((sy * H + sx0) * C + c0) * ES);
+  const Off lane_z = static_cast<Off>(c0 * ES);
+  const Off tap_b = static_cast<Off>(C * ES);
+  const int64_t row_skip = 3 * H * C;
   const int64_t cb = static_cast<int64_t>(blockIdx.x) * cpb;
   const int64_t ce = std::min(ncells, cb + cpb);
+  CellWalk cw;
+  cw.init(cb, G, C);
   for (int64_t cell = cb; cell < ce; ++cell) {
-    const int64_t o = tap_offset(cell, G, C, sy, sx0, c0);
-    float h[TPT][4];
+    const Off ho = static_cast<Off>(cw.hoff * ES) + lane_h;
+    const Off zo = static_cast<Off>(cw.zoff * ES) + lane_z;
+    cw.next(G, C, row_skip);
+    Raw<DT, CPT> hr[TPT];
+    Raw<DT, CPT> dr[LMAX];
 #pragma unroll
-    for (int j = 0; j < TPT; ++j) load_vec<DT, 4>(high, o + j * C, h[j]);
-    const int64_t zo = cell * C + c0;
+    for (int j = 0; j < TPT; ++j) load_at<DT, CPT, NT>(high, ho + j * tap_b, hr[j]);
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) load_at<DT, CPT>(low.p[l < L ? l : 0], zo, dr[l]);
+    LTHC_PHASE_BARRIER();
+    float h[TPT][CPT];
+#pragma unroll
+    for (int j = 0; j < TPT; ++j) unpack_raw<DT, CPT>(hr[j], h[j]);
 #pragma unroll
     for (int l = 0; l < LMAX; ++l) {
-      if (l < L) {
-        float d[4];
-        load_vec<DT, 4>(low.p[l], zo, d);
+      float d[CPT];
+      unpack_raw<DT, CPT>(dr[l], d);
 #pragma unroll
-        for (int j = 0; j < TPT; ++j)
+      for (int j = 0; j < TPT; ++j)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[l][j][v] = fmaf(h[j][v], d[v], acc[l][j][v]);
-      }
+        for (int v = 0; v < CPT; ++v) acc[l][j][v] = fmaf(h[j][v], d[v], acc[l][j][v]);
     }
   }
   float* dst = partial + static_cast<int64_t>(blockIdx.x) * L * C * kK;
@@ -365,7 +509,7 @@ __global__ __launch_bounds__(kBlock) void wgrad_partial_kernel(const void* __res
   for (int l = 0; l < LMAX; ++l) {
     if (l < L) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
+      for (int v = 0; v < CPT; ++v) {
         float* row = dst + (static_cast<int64_t>(l) * C + c0 + v) * kK + tap0;
         if constexpr (TPT == 4) {
           *reinterpret_cast<float4*>(row) = make_float4(acc[l][0][v], acc[l][1][v], acc[l][2][v], acc[l][3][v]);
@@ -396,7 +540,7 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
 }
 
 // ---------------------------------------------------------------------------
-// GAMMA: gamma[l, c] = sum_k alpha[c,k] beta_l[c,k]
+// GAMMA: gamma[l, c] = sum_k alpha[c,k] beta_l[c,k], k = 0..K-1 in order
 // ---------------------------------------------------------------------------
 __global__ __launch_bounds__(256) void gamma_kernel(const void* __restrict__ alpha, PtrPack beta, int wdt,
                                                     void* __restrict__ gamma, int odt, int C, int K, int L) {
@@ -412,12 +556,17 @@ __global__ __launch_bounds__(256) void gamma_kernel(const void* __restrict__ alp
 
 // ---------------------------------------------------------------------------
 // RECURRENCE: z_next = fma(gamma, dz, z).  Block = 64 channel quads x 4 row
-// lanes; each thread keeps its 4 gammas and walks rows with stride 4.
+// lanes; each thread keeps its 4 gammas and walks rows with stride 4, RU
+// rows per phase (loads of rows past the end are clamped to the last row and
+// their results dropped).
 // ---------------------------------------------------------------------------
-template <int DT>
+constexpr int kRU = 4;
+
+template <int DT, typename Off>
 __global__ __launch_bounds__(256) void recur_fwd_kernel(const void* __restrict__ z, const void* __restrict__ dz,
                                                         const void* __restrict__ gamma, int gdt,
                                                         void* __restrict__ zn, int64_t rows, int C, int64_t rpb) {
+  constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int c0 = (blockIdx.x * 64 + (t & 63)) * 4;
   if (c0 >= C) return;
@@ -426,23 +575,36 @@ __global__ __launch_bounds__(256) void recur_fwd_kernel(const void* __restrict__
   for (int v = 0; v < 4; ++v) gm[v] = load_w(gamma, gdt, c0 + v);
   const int64_t rb = static_cast<int64_t>(blockIdx.y) * rpb;
   const int64_t re = std::min(rows, rb + rpb);
-  for (int64_t r = rb + (t >> 6); r < re; r += 4) {
-    const int64_t o = r * C + c0;
-    float a[4], d[4];
-    load_vec<DT, 4>(z, o, a);
-    load_vec<DT, 4>(dz, o, d);
+  for (int64_t r0 = rb + (t >> 6); r0 < re; r0 += 4 * kRU) {
+    Raw<DT, 4> ar[kRU], dr[kRU];
+    Off off[kRU];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) a[v] = fmaf(gm[v], d[v], a[v]);
-    store_vec<DT, 4>(zn, o, a);
+    for (int u = 0; u < kRU; ++u) {
+      const int64_t r = std::min(r0 + 4 * u, re - 1);
+      off[u] = static_cast<Off>((r * C + c0) * ES);
+      load_at<DT, 4>(z, off[u], ar[u]);
+      load_at<DT, 4>(dz, off[u], dr[u]);
+    }
+    LTHC_PHASE_BARRIER();
+#pragma unroll
+    for (int u = 0; u < kRU; ++u) {
+      float a[4], d[4];
+      unpack_raw<DT, 4>(ar[u], a);
+      unpack_raw<DT, 4>(dr[u], d);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) a[v] = fmaf(gm[v], d[v], a[v]);
+      if (r0 + 4 * u < re) store_at<DT, 4>(zn, off[u], a);
+    }
   }
 }
 
 // RECURRENCE BACKWARD: gdz = gamma * g; partial[4*by + lane_row, c] = sum g*dz
-template <int DT>
+template <int DT, typename Off>
 __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__ g, const void* __restrict__ dz,
                                                         const void* __restrict__ gamma, int gdt,
                                                         void* __restrict__ gdz, float* __restrict__ partial,
                                                         int64_t rows, int C, int64_t rpb) {
+  constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int c0 = (blockIdx.x * 64 + (t & 63)) * 4;
   if (c0 >= C) return;
@@ -452,17 +614,31 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
   float s[4] = {0.f, 0.f, 0.f, 0.f};
   const int64_t rb = static_cast<int64_t>(blockIdx.y) * rpb;
   const int64_t re = std::min(rows, rb + rpb);
-  for (int64_t r = rb + (t >> 6); r < re; r += 4) {
-    const int64_t o = r * C + c0;
-    float a[4], d[4], o4[4];
-    load_vec<DT, 4>(g, o, a);
-    load_vec<DT, 4>(dz, o, d);
+  for (int64_t r0 = rb + (t >> 6); r0 < re; r0 += 4 * kRU) {
+    Raw<DT, 4> ar[kRU], dr[kRU];
+    Off off[kRU];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      o4[v] = gm[v] * a[v];
-      s[v] = fmaf(a[v], d[v], s[v]);
+    for (int u = 0; u < kRU; ++u) {
+      const int64_t r = std::min(r0 + 4 * u, re - 1);
+      off[u] = static_cast<Off>((r * C + c0) * ES);
+      load_at<DT, 4, true>(g, off[u], ar[u]);
+      load_at<DT, 4, true>(dz, off[u], dr[u]);
     }
-    store_vec<DT, 4>(gdz, o, o4);
+    LTHC_PHASE_BARRIER();
+#pragma unroll
+    for (int u = 0; u < kRU; ++u) {
+      if (r0 + 4 * u < re) {
+        float a[4], d[4], o4[4];
+        unpack_raw<DT, 4>(ar[u], a);
+        unpack_raw<DT, 4>(dr[u], d);
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          o4[v] = gm[v] * a[v];
+          s[v] = fmaf(a[v], d[v], s[v]);
+        }
+        store_at<DT, 4, true>(gdz, off[u], o4);
+      }
+    }
   }
   float* dst = partial + (static_cast<int64_t>(blockIdx.y) * 4 + (t >> 6)) * C + c0;
   *reinterpret_cast<float4*>(dst) = make_float4(s[0], s[1], s[2], s[3]);
@@ -516,6 +692,17 @@ int check_act(const char* fn, const void* p, int dt, const char* name) {
   return LTHC_OK;
 }
 
+// Weights are read as whole 16-tap rows: 16-byte alignment.
+int check_weight(const char* fn, const void* p, const std::string& name) {
+  if (p == nullptr) return fail(LTHC_ERR_INVALID, fn, name + " is NULL");
+  if (!aligned(p, 16)) return fail(LTHC_ERR_INVALID, fn, name + " is not 16-byte aligned");
+  return LTHC_OK;
+}
+
+// Activation / weight dtype pairs with compiled kernels: weights in fp32 or
+// in the activation dtype.
+bool supported_pair(int x_dtype, int w_dtype) { return w_dtype == LTHC_F32 || w_dtype == x_dtype; }
+
 // Cells per block so that a launch has about `blocks_per_cu` blocks per CU.
 int64_t cells_per_block(int64_t ncells, int64_t slabs, int blocks_per_cu) {
   const int64_t target = std::max<int64_t>(1, static_cast<int64_t>(num_cus()) * blocks_per_cu / std::max<int64_t>(1, slabs));
@@ -530,123 +717,220 @@ struct WgradPlan {
   int64_t nbx;
 };
 
-WgradPlan wgrad_plan(int64_t ncells, int64_t C, int L) {
+template <int LMAX>
+struct CellShape;
+
+// (TPT, CPT) of the weight-gradient kernel for depth L (the CellShape bucket).
+void wgrad_shape(int L, int& tpt, int& cpt);
+
+WgradPlan wgrad_plan(int64_t ncells, int64_t C, int L, int blocks_per_cu = 2) {
   WgradPlan p;
-  p.tpt = L <= 12 ? 4 : (L <= 24 ? 2 : 1);
+  int cpt = 4;
+  wgrad_shape(L, p.tpt, cpt);
   const int qs = kBlock / (kK / p.tpt);
-  p.slabs = static_cast<int>((C / 4 + qs - 1) / qs);
-  p.cpb = cells_per_block(ncells, p.slabs, 2);
+  p.slabs = static_cast<int>((C / cpt + qs - 1) / qs);
+  p.cpb = cells_per_block(ncells, p.slabs, blocks_per_cu);
   p.nbx = ncells > 0 ? (ncells + p.cpb - 1) / p.cpb : 0;
   return p;
 }
 
-const int64_t kRecurRowsPerBlock = 256;
+// Rows per block of the recurrence kernels (forward: more, smaller blocks
+// measured faster; backward: fewer partial rows to reduce).
+const int64_t kRecurRowsPerBlock = 64;
+const int64_t kRecurBwdRowsPerBlock = 256;
 
-template <int DT>
-void launch_read(const void* x, const void* w, int wdt, void* z, int64_t ncells, int G, int C, bool vec8,
-                 hipStream_t st) {
+template <int V>
+using IC = std::integral_constant<int, V>;
+
+template <typename T>
+struct TypeTag {
+  using type = T;
+};
+
+// Calls f(IC<DT>, IC<WDT>) for a supported (activation, weight) dtype pair.
+template <typename F>
+void dispatch_pair(int xdt, int wdt, F&& f) {
+  switch (xdt) {
+    case LTHC_F32: f(IC<LTHC_F32>{}, IC<LTHC_F32>{}); break;
+    case LTHC_BF16:
+      if (wdt == LTHC_F32) f(IC<LTHC_BF16>{}, IC<LTHC_F32>{});
+      else f(IC<LTHC_BF16>{}, IC<LTHC_BF16>{});
+      break;
+    default:
+      if (wdt == LTHC_F32) f(IC<LTHC_F16>{}, IC<LTHC_F32>{});
+      else f(IC<LTHC_F16>{}, IC<LTHC_F16>{});
+      break;
+  }
+}
+
+template <typename F>
+void dispatch_dtype(int dt, F&& f) {
+  switch (dt) {
+    case LTHC_F32: f(IC<LTHC_F32>{}); break;
+    case LTHC_BF16: f(IC<LTHC_BF16>{}); break;
+    default: f(IC<LTHC_F16>{}); break;
+  }
+}
+
+// 32-bit byte offsets when every tensor of the call is below 4 GiB.
+bool fits32(int64_t bytes) { return bytes < (int64_t(1) << 32); }
+
+template <typename F>
+void dispatch_off(bool off32, F&& f) {
+  if (off32) f(TypeTag<uint32_t>{});
+  else f(TypeTag<int64_t>{});
+}
+
+constexpr int kReadBlocksPerCU = 8;
+
+template <int DT, int WDT, typename Off>
+void launch_read(const void* x, const void* w, void* z, int64_t ncells, int G, int C, bool vec8, hipStream_t st,
+                 int blocks_per_cu = kReadBlocksPerCU) {
   const int vec = vec8 ? 8 : 4;
   const int ncv = C / vec;
   const int ncv_blk = std::min(ncv, kBlock);
   const int cpi = kBlock / ncv_blk;
   const int gy = (ncv + ncv_blk - 1) / ncv_blk;
-  const int64_t cpb = std::max<int64_t>(cpi, cells_per_block(ncells, gy, 8));
+  const int64_t cpb = std::max<int64_t>(cpi, cells_per_block(ncells, gy, blocks_per_cu));
   const dim3 grid(static_cast<unsigned>((ncells + cpb - 1) / cpb), gy);
   const dim3 block(ncv_blk * cpi);
-  if (vec8) {
-    if constexpr (DT != LTHC_F32)
-      read_fwd_kernel<DT, 8><<<grid, block, 0, st>>>(x, w, wdt, z, ncells, G, C, ncv_blk, cpi, cpb);
-  } else {
-    read_fwd_kernel<DT, 4><<<grid, block, 0, st>>>(x, w, wdt, z, ncells, G, C, ncv_blk, cpi, cpb);
+  if constexpr (DT != LTHC_F32) {
+    if (vec8) {
+      read_fwd_kernel<DT, WDT, 8, Off><<<grid, block, 0, st>>>(x, w, z, ncells, G, C, ncv_blk, cpi, cpb);
+      return;
+    }
   }
+  read_fwd_kernel<DT, WDT, 4, Off><<<grid, block, 0, st>>>(x, w, z, ncells, G, C, ncv_blk, cpi, cpb);
 }
 
-template <int DT, int LMAX, int TPT>
-void launch_materialise_t(const void* base, const PtrPack& dz, const PtrPack& beta, int wdt, void* out, int L,
-                          int64_t ncells, int G, int C, hipStream_t st) {
+// Thread shapes (taps x channels per thread) of the register-resident weight
+// kernels, per depth bucket: the weights (LMAX x TPT x CPT fp32) plus one
+// cell's loads must fit in 256 VGPRs with two or more waves per SIMD.
+template <int LMAX>
+struct CellShape {
+  static constexpr int TPT = LMAX <= 8 ? 4 : (LMAX <= 16 ? 4 : (LMAX <= 32 ? 2 : 1));
+  static constexpr int CPT = LMAX <= 8 ? 4 : 2;
+};
+void wgrad_shape(int L, int& tpt, int& cpt) {
+#define LTHC_WS(LM)              \
+  {                              \
+    tpt = CellShape<LM>::TPT;    \
+    cpt = CellShape<LM>::CPT;    \
+    return;                      \
+  }
+  if (L <= 1) LTHC_WS(1);
+  if (L <= 2) LTHC_WS(2);
+  if (L <= 4) LTHC_WS(4);
+  if (L <= 8) LTHC_WS(8);
+  if (L <= 12) LTHC_WS(12);
+  if (L <= 16) LTHC_WS(16);
+  if (L <= 24) LTHC_WS(24);
+  if (L <= 32) LTHC_WS(32);
+  LTHC_WS(48);
+#undef LTHC_WS
+}
+
+constexpr int kMatBlocksPerCU = 6;
+
+template <int DT, int WDT, int LMAX, int TPT, int CPT, bool HAS_BASE, bool EXACT, bool NT, typename Off>
+void launch_mat_t(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells, int G,
+                  int C, int blocks_per_cu, hipStream_t st) {
   constexpr int QS = kBlock / (kK / TPT);
-  const int slabs = (C / 4 + QS - 1) / QS;
-  const int64_t cpb = cells_per_block(ncells, slabs, 8);
+  const int slabs = (C / CPT + QS - 1) / QS;
+  const int64_t cpb = cells_per_block(ncells, slabs, blocks_per_cu);
   const dim3 grid(static_cast<unsigned>((ncells + cpb - 1) / cpb), slabs);
-  materialise_kernel<DT, LMAX, TPT><<<grid, kBlock, 0, st>>>(base, dz, beta, wdt, out, L, ncells, G, C, cpb);
+  materialise_kernel<DT, WDT, LMAX, TPT, CPT, HAS_BASE, EXACT, NT, Off>
+      <<<grid, kBlock, 0, st>>>(base, dz, beta, out, L, ncells, G, C, cpb);
 }
 
-template <int DT>
-void launch_materialise(const void* base, const PtrPack& dz, const PtrPack& beta, int wdt, void* out, int L,
-                        int64_t ncells, int G, int C, hipStream_t st) {
-#define LTHC_MAT(LM, TP) launch_materialise_t<DT, LM, TP>(base, dz, beta, wdt, out, L, ncells, G, C, st)
-  if (L <= 1) LTHC_MAT(1, 4);
-  else if (L <= 2) LTHC_MAT(2, 4);
-  else if (L <= 4) LTHC_MAT(4, 4);
-  else if (L <= 8) LTHC_MAT(8, 4);
-  else if (L <= 12) LTHC_MAT(12, 4);
-  else if (L <= 16) LTHC_MAT(16, 2);
-  else if (L <= 24) LTHC_MAT(24, 2);
-  else if (L <= 32) LTHC_MAT(32, 1);
-  else LTHC_MAT(48, 1);
-#undef LTHC_MAT
+template <int DT, int WDT, int LMAX>
+void launch_mat_l(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells, int G,
+                  int C, bool off32, hipStream_t st) {
+  constexpr int TPT = CellShape<LMAX>::TPT, CPT = CellShape<LMAX>::CPT;
+  if (!off32)  // tensors of 4 GiB and more: 64-bit offsets, any depth in the bucket
+    launch_mat_t<DT, WDT, LMAX, TPT, CPT, true, false, true, int64_t>(base, dz, beta, out, L, ncells, G, C, kMatBlocksPerCU, st);
+  else if (L == LMAX)
+    launch_mat_t<DT, WDT, LMAX, TPT, CPT, true, true, true, uint32_t>(base, dz, beta, out, L, ncells, G, C, kMatBlocksPerCU, st);
+  else
+    launch_mat_t<DT, WDT, LMAX, TPT, CPT, true, false, true, uint32_t>(base, dz, beta, out, L, ncells, G, C, kMatBlocksPerCU, st);
 }
 
-template <int DT, int LMAX, int TPT>
+template <int DT, int WDT>
+void launch_materialise(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells,
+                        int G, int C, hipStream_t st) {
+  const bool off32 = fits32(ncells * kK * C * Fmt<DT>::bytes);
+  if (base == nullptr) {  // the plain write: one layer, no base (validated by the caller)
+    dispatch_off(off32, [&](auto o) {
+      launch_mat_t<DT, WDT, 1, 4, 4, false, true, true, typename decltype(o)::type>(base, dz, beta, out, 1, ncells, G,
+                                                                                    C, kMatBlocksPerCU, st);
+    });
+    return;
+  }
+  if (L <= 1) launch_mat_l<DT, WDT, 1>(base, dz, beta, out, L, ncells, G, C, off32, st);
+  else if (L <= 2) launch_mat_l<DT, WDT, 2>(base, dz, beta, out, L, ncells, G, C, off32, st);
+  else if (L <= 4) launch_mat_l<DT, WDT, 4>(base, dz, beta, out, L, ncells, G, C, off32, st);
+  else if (L <= 8) launch_mat_l<DT, WDT, 8>(base, dz, beta, out, L, ncells, G, C, off32, st);
+  else if (L <= 12) launch_mat_l<DT, WDT, 12>(base, dz, beta, out, L, ncells, G, C, off32, st);
+  else if (L <= 16) launch_mat_l<DT, WDT, 16>(base, dz, beta, out, L, ncells, G, C, off32, st);
+  else if (L <= 24) launch_mat_l<DT, WDT, 24>(base, dz, beta, out, L, ncells, G, C, off32, st);
+  else if (L <= 32) launch_mat_l<DT, WDT, 32>(base, dz, beta, out, L, ncells, G, C, off32, st);
+  else launch_mat_l<DT, WDT, 48>(base, dz, beta, out, L, ncells, G, C, off32, st);
+}
+
+template <int DT, int LMAX, int TPT, int CPT, bool NT, typename Off>
 void launch_wgrad_t(const void* high, const PtrPack& low, float* partial, int L, int64_t ncells, int G, int C,
                     const WgradPlan& p, hipStream_t st) {
   const dim3 grid(static_cast<unsigned>(p.nbx), p.slabs);
-  wgrad_partial_kernel<DT, LMAX, TPT><<<grid, kBlock, 0, st>>>(high, low, partial, L, ncells, G, C, p.cpb);
+  wgrad_partial_kernel<DT, LMAX, TPT, CPT, NT, Off><<<grid, kBlock, 0, st>>>(high, low, partial, L, ncells, G, C, p.cpb);
 }
 
-template <int DT>
+template <int DT, typename Off>
 void launch_wgrad(const void* high, const PtrPack& low, float* partial, int L, int64_t ncells, int G, int C,
                   const WgradPlan& p, hipStream_t st) {
-#define LTHC_WG(LM, TP) launch_wgrad_t<DT, LM, TP>(high, low, partial, L, ncells, G, C, p, st)
-  if (L <= 1) LTHC_WG(1, 4);
-  else if (L <= 2) LTHC_WG(2, 4);
-  else if (L <= 4) LTHC_WG(4, 4);
-  else if (L <= 8) LTHC_WG(8, 4);
-  else if (L <= 12) LTHC_WG(12, 4);
-  else if (L <= 16) LTHC_WG(16, 2);
-  else if (L <= 24) LTHC_WG(24, 2);
-  else if (L <= 32) LTHC_WG(32, 1);
-  else LTHC_WG(48, 1);
+#define LTHC_WG(LM) \
+  launch_wgrad_t<DT, LM, CellShape<LM>::TPT, CellShape<LM>::CPT, true, Off>(high, low, partial, L, ncells, G, C, p, st)
+  if (L <= 1) LTHC_WG(1);
+  else if (L <= 2) LTHC_WG(2);
+  else if (L <= 4) LTHC_WG(4);
+  else if (L <= 8) LTHC_WG(8);
+  else if (L <= 12) LTHC_WG(12);
+  else if (L <= 16) LTHC_WG(16);
+  else if (L <= 24) LTHC_WG(24);
+  else if (L <= 32) LTHC_WG(32);
+  else LTHC_WG(48);
 #undef LTHC_WG
 }
 
-template <int DT, int LC>
-void launch_read_multi_t(const void* g, const PtrPack& w, int wdt, const PtrPack& out, int L, int64_t ncells, int G,
-                         int C, hipStream_t st) {
+template <int DT, int WDT, int LC, typename Off>
+void launch_read_multi_t(const void* g, const PtrPack& w, const PtrPack& out, int L, int64_t ncells, int G, int C,
+                         hipStream_t st) {
   const int nlg = (L + LC - 1) / LC;
   const int qs = std::max(16, (kBlock / nlg) / 16 * 16);  // qs * nlg <= 256 for nlg <= 16
   const int slabs = (C / 4 + qs - 1) / qs;
   const int64_t cpb = cells_per_block(ncells, slabs, 8);
   const dim3 grid(static_cast<unsigned>((ncells + cpb - 1) / cpb), slabs);
-  read_multi_kernel<DT, LC><<<grid, qs * nlg, 0, st>>>(g, w, wdt, out, L, qs, ncells, G, C, cpb);
+  read_multi_kernel<DT, WDT, LC, Off><<<grid, qs * nlg, 0, st>>>(g, w, out, L, qs, ncells, G, C, cpb);
 }
 
-template <int DT>
-void launch_read_multi(const void* g, const PtrPack& w, int wdt, const PtrPack& out, int L, int64_t ncells, int G,
-                       int C, hipStream_t st) {
-  // Two layers per thread keep the 128 weights + accumulators within 256
-  // VGPRs (3 would spill); 3 per thread only where 16 groups of 2 are not enough.
-  if (L == 1) launch_read_multi_t<DT, 1>(g, w, wdt, out, L, ncells, G, C, st);
-  else if (L <= 32) launch_read_multi_t<DT, 2>(g, w, wdt, out, L, ncells, G, C, st);
-  else launch_read_multi_t<DT, 3>(g, w, wdt, out, L, ncells, G, C, st);
-}
-
-template <typename F>
-int dispatch_dtype(int dt, F&& f) {
-  switch (dt) {
-    case LTHC_F32: f(std::integral_constant<int, LTHC_F32>{}); return LTHC_OK;
-    case LTHC_BF16: f(std::integral_constant<int, LTHC_BF16>{}); return LTHC_OK;
-    case LTHC_F16: f(std::integral_constant<int, LTHC_F16>{}); return LTHC_OK;
-    default: return LTHC_ERR_INVALID;
-  }
+template <int DT, int WDT, typename Off>
+void launch_read_multi(const void* g, const PtrPack& w, const PtrPack& out, int L, int64_t ncells, int G, int C,
+                       hipStream_t st) {
+  // Two layers per thread keep 128 weights + loads + accumulators within 256
+  // VGPRs; three per thread only where 16 groups of two are not enough.
+  if (L == 1) launch_read_multi_t<DT, WDT, 1, Off>(g, w, out, L, ncells, G, C, st);
+  else if (L <= 32) launch_read_multi_t<DT, WDT, 2, Off>(g, w, out, L, ncells, G, C, st);
+  else launch_read_multi_t<DT, WDT, 3, Off>(g, w, out, L, ncells, G, C, st);
 }
 
 int fill_ptrs(const char* fn, PtrPack& pk, const void* const* src, int L, const char* name, int dt, bool act) {
   if (src == nullptr) return fail(LTHC_ERR_INVALID, fn, std::string(name) + " pointer array is NULL");
   for (int l = 0; l < L; ++l) {
-    if (src[l] == nullptr) return fail(LTHC_ERR_INVALID, fn, std::string(name) + "[" + std::to_string(l) + "] is NULL");
-    if (act && !aligned(src[l], 4 * esize(dt)))
-      return fail(LTHC_ERR_INVALID, fn, std::string(name) + "[" + std::to_string(l) + "] is not aligned to 4 elements");
+    const std::string nm = std::string(name) + "[" + std::to_string(l) + "]";
+    if (act) {
+      if (int rc = check_act(fn, src[l], dt, nm.c_str())) return rc;
+    } else {
+      if (int rc = check_weight(fn, src[l], nm)) return rc;
+    }
     pk.p[l] = src[l];
   }
   for (int l = L; l < LTHC_MAX_LAYERS; ++l) pk.p[l] = nullptr;
@@ -656,6 +940,13 @@ int fill_ptrs(const char* fn, PtrPack& pk, const void* const* src, int L, const 
 int check_layers(const char* fn, int L) {
   if (L < 1) return fail(LTHC_ERR_INVALID, fn, "L must be >= 1");
   if (L > LTHC_MAX_LAYERS) return fail(LTHC_ERR_UNSUPPORTED, fn, "L exceeds LTHC_MAX_LAYERS");
+  return LTHC_OK;
+}
+
+int check_pair(const char* fn, int x_dtype, int w_dtype) {
+  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype)) return fail(LTHC_ERR_INVALID, fn, "unknown dtype code");
+  if (!supported_pair(x_dtype, w_dtype))
+    return fail(LTHC_ERR_UNSUPPORTED, fn, "weights must be fp32 or have the activation dtype");
   return LTHC_OK;
 }
 
@@ -675,16 +966,19 @@ int lthc_read_fwd(const void* x, int x_dtype, const void* alpha, int w_dtype, vo
   static const char* fn = "lthc_read_fwd";
   g_last_error.clear();
   if (int rc = check_geom(fn, B, G, s, C)) return rc;
-  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype)) return fail(LTHC_ERR_INVALID, fn, "unknown dtype code");
+  if (int rc = check_pair(fn, x_dtype, w_dtype)) return rc;
   if (B == 0) return LTHC_OK;
   if (int rc = check_act(fn, x, x_dtype, "x")) return rc;
   if (int rc = check_act(fn, z, x_dtype, "z")) return rc;
-  if (alpha == nullptr) return fail(LTHC_ERR_INVALID, fn, "alpha is NULL");
+  if (int rc = check_weight(fn, alpha, "alpha")) return rc;
   const int64_t ncells = B * G * G;
   const bool vec8 = x_dtype != LTHC_F32 && C % 8 == 0 && aligned(x, 16) && aligned(z, 16);
-  dispatch_dtype(x_dtype, [&](auto d) {
-    launch_read<decltype(d)::value>(x, alpha, w_dtype, z, ncells, static_cast<int>(G), static_cast<int>(C), vec8,
-                                    static_cast<hipStream_t>(stream));
+  const bool off32 = fits32(ncells * kK * C * esize(x_dtype));
+  dispatch_pair(x_dtype, w_dtype, [&](auto d, auto wd) {
+    dispatch_off(off32, [&](auto o) {
+      launch_read<decltype(d)::value, decltype(wd)::value, typename decltype(o)::type>(
+          x, alpha, z, ncells, static_cast<int>(G), static_cast<int>(C), vec8, static_cast<hipStream_t>(stream));
+    });
   });
   return check_launch(fn);
 }
@@ -695,16 +989,19 @@ int lthc_read_multi_fwd(const void* g, int x_dtype, const void* const* w, int w_
   g_last_error.clear();
   if (int rc = check_geom(fn, B, G, s, C)) return rc;
   if (int rc = check_layers(fn, L)) return rc;
-  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype)) return fail(LTHC_ERR_INVALID, fn, "unknown dtype code");
+  if (int rc = check_pair(fn, x_dtype, w_dtype)) return rc;
   if (B == 0) return LTHC_OK;
   if (int rc = check_act(fn, g, x_dtype, "g")) return rc;
   PtrPack wp, op;
   if (int rc = fill_ptrs(fn, wp, w, L, "w", w_dtype, false)) return rc;
   if (int rc = fill_ptrs(fn, op, const_cast<const void* const*>(out), L, "out", x_dtype, true)) return rc;
   const int64_t ncells = B * G * G;
-  dispatch_dtype(x_dtype, [&](auto d) {
-    launch_read_multi<decltype(d)::value>(g, wp, w_dtype, op, L, ncells, static_cast<int>(G), static_cast<int>(C),
-                                          static_cast<hipStream_t>(stream));
+  const bool off32 = fits32(ncells * kK * C * esize(x_dtype));
+  dispatch_pair(x_dtype, w_dtype, [&](auto d, auto wd) {
+    dispatch_off(off32, [&](auto o) {
+      launch_read_multi<decltype(d)::value, decltype(wd)::value, typename decltype(o)::type>(
+          g, wp, op, L, ncells, static_cast<int>(G), static_cast<int>(C), static_cast<hipStream_t>(stream));
+    });
   });
   return check_launch(fn);
 }
@@ -715,7 +1012,8 @@ int lthc_materialise_fwd(const void* base, const void* const* dz, int x_dtype, c
   g_last_error.clear();
   if (int rc = check_geom(fn, B, G, s, C)) return rc;
   if (int rc = check_layers(fn, L)) return rc;
-  if (!valid_dtype(x_dtype) || !valid_dtype(w_dtype)) return fail(LTHC_ERR_INVALID, fn, "unknown dtype code");
+  if (int rc = check_pair(fn, x_dtype, w_dtype)) return rc;
+  if (base == nullptr && L != 1) return fail(LTHC_ERR_UNSUPPORTED, fn, "base == NULL is implemented for L == 1 only");
   if (B == 0) return LTHC_OK;
   if (base != nullptr)
     if (int rc = check_act(fn, base, x_dtype, "base")) return rc;
@@ -724,9 +1022,9 @@ int lthc_materialise_fwd(const void* base, const void* const* dz, int x_dtype, c
   if (int rc = fill_ptrs(fn, dp, dz, L, "dz", x_dtype, true)) return rc;
   if (int rc = fill_ptrs(fn, bp, beta, L, "beta", w_dtype, false)) return rc;
   const int64_t ncells = B * G * G;
-  dispatch_dtype(x_dtype, [&](auto d) {
-    launch_materialise<decltype(d)::value>(base, dp, bp, w_dtype, out, L, ncells, static_cast<int>(G),
-                                           static_cast<int>(C), static_cast<hipStream_t>(stream));
+  dispatch_pair(x_dtype, w_dtype, [&](auto d, auto wd) {
+    launch_materialise<decltype(d)::value, decltype(wd)::value>(base, dp, bp, out, L, ncells, static_cast<int>(G),
+                                                                static_cast<int>(C), static_cast<hipStream_t>(stream));
   });
   return check_launch(fn);
 }
@@ -761,8 +1059,12 @@ int lthc_weight_grad(const void* high, const void* const* low, int x_dtype, floa
     return fail(LTHC_ERR_INVALID, fn, "workspace smaller than lthc_weight_grad_workspace_bytes()");
   if (!aligned(workspace, 16)) return fail(LTHC_ERR_INVALID, fn, "workspace is not 16-byte aligned");
   float* partial = static_cast<float*>(workspace);
+  const bool off32 = fits32(ncells * kK * C * esize(x_dtype));
   dispatch_dtype(x_dtype, [&](auto d) {
-    launch_wgrad<decltype(d)::value>(high, lp, partial, L, ncells, static_cast<int>(G), static_cast<int>(C), p, st);
+    dispatch_off(off32, [&](auto o) {
+      launch_wgrad<decltype(d)::value, typename decltype(o)::type>(high, lp, partial, L, ncells, static_cast<int>(G),
+                                                                   static_cast<int>(C), p, st);
+    });
   });
   if (int rc = check_launch(fn)) return rc;
   reduce_partials_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(partial, static_cast<int>(p.nbx), n, gw);
@@ -778,7 +1080,11 @@ int lthc_gamma(const void* alpha, const void* const* beta, int w_dtype, void* ga
   if (!valid_dtype(w_dtype) || !valid_dtype(out_dtype)) return fail(LTHC_ERR_INVALID, fn, "unknown dtype code");
   if (alpha == nullptr || gamma == nullptr) return fail(LTHC_ERR_INVALID, fn, "alpha or gamma is NULL");
   PtrPack bp;
-  if (int rc = fill_ptrs(fn, bp, beta, L, "beta", w_dtype, false)) return rc;
+  if (beta == nullptr) return fail(LTHC_ERR_INVALID, fn, "beta pointer array is NULL");
+  for (int l = 0; l < L; ++l) {
+    if (beta[l] == nullptr) return fail(LTHC_ERR_INVALID, fn, "beta[" + std::to_string(l) + "] is NULL");
+    bp.p[l] = beta[l];
+  }
   const int64_t n = static_cast<int64_t>(L) * C;
   gamma_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
       alpha, bp, w_dtype, gamma, out_dtype, static_cast<int>(C), static_cast<int>(K), L);
@@ -798,16 +1104,19 @@ int lthc_recur_fwd(const void* z, const void* dz, int x_dtype, const void* gamma
   if (gamma == nullptr) return fail(LTHC_ERR_INVALID, fn, "gamma is NULL");
   const dim3 grid(static_cast<unsigned>((C / 4 + 63) / 64), static_cast<unsigned>((rows + kRecurRowsPerBlock - 1) / kRecurRowsPerBlock));
   const hipStream_t st = static_cast<hipStream_t>(stream);
+  const bool off32 = fits32(rows * C * esize(x_dtype));
   dispatch_dtype(x_dtype, [&](auto d) {
-    recur_fwd_kernel<decltype(d)::value><<<grid, 256, 0, st>>>(z, dz, gamma, g_dtype, z_next, rows, static_cast<int>(C),
-                                                               kRecurRowsPerBlock);
+    dispatch_off(off32, [&](auto o) {
+      recur_fwd_kernel<decltype(d)::value, typename decltype(o)::type>
+          <<<grid, 256, 0, st>>>(z, dz, gamma, g_dtype, z_next, rows, static_cast<int>(C), kRecurRowsPerBlock);
+    });
   });
   return check_launch(fn);
 }
 
 size_t lthc_recur_bwd_workspace_bytes(int64_t rows, int64_t C) {
   if (rows <= 0 || C <= 0) return 0;
-  const int64_t by = (rows + kRecurRowsPerBlock - 1) / kRecurRowsPerBlock;
+  const int64_t by = (rows + kRecurBwdRowsPerBlock - 1) / kRecurBwdRowsPerBlock;
   return static_cast<size_t>(by * 4 * C) * sizeof(float);
 }
 
@@ -830,12 +1139,15 @@ int lthc_recur_bwd(const void* g, const void* dz, int x_dtype, const void* gamma
   if (workspace == nullptr || workspace_bytes < need)
     return fail(LTHC_ERR_INVALID, fn, "workspace smaller than lthc_recur_bwd_workspace_bytes()");
   if (!aligned(workspace, 16)) return fail(LTHC_ERR_INVALID, fn, "workspace is not 16-byte aligned");
-  const int64_t by = (rows + kRecurRowsPerBlock - 1) / kRecurRowsPerBlock;
+  const int64_t by = (rows + kRecurBwdRowsPerBlock - 1) / kRecurBwdRowsPerBlock;
   const dim3 grid(static_cast<unsigned>((C / 4 + 63) / 64), static_cast<unsigned>(by));
   float* partial = static_cast<float*>(workspace);
+  const bool off32 = fits32(rows * C * esize(x_dtype));
   dispatch_dtype(x_dtype, [&](auto d) {
-    recur_bwd_kernel<decltype(d)::value><<<grid, 256, 0, st>>>(g, dz, gamma, g_dtype, gdz, partial, rows,
-                                                               static_cast<int>(C), kRecurRowsPerBlock);
+    dispatch_off(off32, [&](auto o) {
+      recur_bwd_kernel<decltype(d)::value, typename decltype(o)::type>
+          <<<grid, 256, 0, st>>>(g, dz, gamma, g_dtype, gdz, partial, rows, static_cast<int>(C), kRecurBwdRowsPerBlock);
+    });
   });
   if (int rc = check_launch(fn)) return rc;
   reduce_partials_kernel<<<static_cast<unsigned>((C + 255) / 256), 256, 0, st>>>(partial, static_cast<int>(by * 4), C, ggamma);

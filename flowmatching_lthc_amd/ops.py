@@ -55,6 +55,16 @@ def _prep(t: Tensor) -> Tensor:
     return t
 
 
+def _prep_w(w: Tensor, act_dtype: torch.dtype) -> Tensor:
+    """Weights in fp32 or the activation dtype (the compiled pairs), contiguous, 16-byte aligned."""
+    if w.dtype not in (torch.float32, act_dtype):
+        w = w.float()
+    w = w.contiguous()
+    if w.data_ptr() % 16 != 0:
+        w = w.clone()
+    return w
+
+
 def _hi_geom(x: Tensor, name: str = "x") -> tuple[int, int, int]:
     if x.dim() != 4 or x.shape[1] != x.shape[2]:
         raise ValueError(f"{name} must be NHWC [B,H,H,C], got {tuple(x.shape)}")
@@ -144,7 +154,8 @@ def local_write_traceable(x: Tensor, weight: Tensor) -> Tensor:
     _on_gpu(x, weight)
     b, g, c = _hi_geom(x)
     _check_weight(weight, c, "weight")
-    x, w = _prep(x), _prep(weight)
+    x = _prep(x)
+    w = _prep_w(weight, x.dtype)
     z = torch.empty((b, g * g, c), device=x.device, dtype=x.dtype)
     _launch_read(x, w, z, b, g, c)
     return z
@@ -165,7 +176,8 @@ def local_read_traceable(z: Tensor, weight: Tensor) -> Tensor:
     _on_gpu(z, weight)
     b, g, c = _lo_geom(z)
     _check_weight(weight, c, "weight")
-    z, w = _prep(z), _prep(weight)
+    z = _prep(z)
+    w = _prep_w(weight, z.dtype)
     out = torch.empty((b, g * S, g * S, c), device=z.device, dtype=z.dtype)
     _launch_materialise(None, [z], [w], out)
     return out
@@ -251,7 +263,7 @@ def final_accumulate_b4_traceable(x0: Tensor, dz_stack: Tensor, beta_stack: Tens
     _check_stack(x0, dz_stack, beta_stack)
     x0 = _prep(x0)
     (dz_stack,) = _same_dtype(x0, [_prep(dz_stack)])
-    beta_stack = _prep(beta_stack)
+    beta_stack = _prep_w(beta_stack, x0.dtype)
     out = torch.empty_like(x0)
     _launch_materialise(x0, list(dz_stack.unbind(0)), list(beta_stack.unbind(0)), out)
     return out
@@ -270,7 +282,8 @@ def final_accumulate_b4_grad_dz_traceable(grad_out: Tensor, beta_stack: Tensor) 
     L = beta_stack.shape[0]
     if beta_stack.dim() != 3 or tuple(beta_stack.shape[1:]) != (c, K) or not 1 <= L <= _abi.MAX_LAYERS:
         raise ValueError(f"beta_stack must be [L,{c},{K}] with 1 <= L <= {_abi.MAX_LAYERS}, got {tuple(beta_stack.shape)}")
-    grad_out, beta_stack = _prep(grad_out), _prep(beta_stack)
+    grad_out = _prep(grad_out)
+    beta_stack = _prep_w(beta_stack, grad_out.dtype)
     gdz = torch.empty((L, b, g * g, c), device=grad_out.device, dtype=grad_out.dtype)
     _launch_read_multi(grad_out, list(beta_stack.unbind(0)), list(gdz.unbind(0)))
     return gdz
@@ -346,9 +359,9 @@ def final_accumulate_b4_12_traceable(
     _check_12(x0, dzs, betas)
     x0 = _prep(x0)
     dzs = _same_dtype(x0, [_prep(d) for d in dzs])
-    betas = [_prep(bt) for bt in betas]
+    betas = [_prep_w(bt, x0.dtype) for bt in betas]
     if len({bt.dtype for bt in betas}) != 1:
-        betas = [bt.float() for bt in betas]
+        betas = [_prep_w(bt.float(), x0.dtype) for bt in betas]
     out = torch.empty_like(x0)
     _launch_materialise(x0, dzs, betas, out)
     return out
@@ -372,9 +385,9 @@ def final_accumulate_b4_12_grad_dz_ptr_traceable(
     for i, bt in enumerate(betas):
         _check_weight(bt, c, f"beta{i}")
     grad_out = _prep(grad_out)
-    betas = [_prep(bt) for bt in betas]
+    betas = [_prep_w(bt, grad_out.dtype) for bt in betas]
     if len({bt.dtype for bt in betas}) != 1:
-        betas = [bt.float() for bt in betas]
+        betas = [_prep_w(bt.float(), grad_out.dtype) for bt in betas]
     gdz = torch.empty((12, b, g * g, c), device=grad_out.device, dtype=grad_out.dtype)
     _launch_read_multi(grad_out, betas, list(gdz.unbind(0)))
     return gdz

@@ -12,8 +12,9 @@
  *
  * Conventions shared by every entry point
  *   - All tensors are dense, row-major, in device memory of the current HIP
- *     device.  Pointers must be aligned to 4 elements (8 bytes for 16-bit
- *     types, 16 bytes for fp32) and C must be a multiple of 4.
+ *     device.  Activation pointers must be aligned to 4 elements (8 bytes for
+ *     16-bit types, 16 bytes for fp32), weight pointers to 16 bytes, and C
+ *     must be a multiple of 4.
  *   - Geometry: B batch, G workspace grid side, s cell side (taps K = s*s),
  *     C channels.  High-resolution grid side H = G*s.  Cells M = G*G.
  *       x  (high-res)  [B, H, H, C]   (NHWC; cell view [B, M, K, C] is logical)
@@ -24,7 +25,8 @@
  *     Only s == 4 is implemented (K = 16, the B/4 model and the 512px
  *     stress configuration); other values return LTHC_ERR_UNSUPPORTED.
  *   - dtype codes: LTHC_F32, LTHC_BF16, LTHC_F16.  Activations share one
- *     dtype per call; weights carry their own dtype.  All arithmetic is fp32
+ *     dtype per call; weights are fp32 or the activation dtype (other pairs
+ *     return LTHC_ERR_UNSUPPORTED; lthc_gamma takes any).  All arithmetic is fp32
  *     (fused multiply-add), results are rounded once (round-to-nearest-even)
  *     to the output dtype.
  *   - Every call is asynchronous on `stream` (a hipStream_t; NULL = the null
@@ -89,7 +91,8 @@ int lthc_read_multi_fwd(const void* g, int x_dtype, const void* const* w, int w_
 /*
  * MATERIALISE / WRITE
  *   out[b,m,k,c] = base[b,m,k,c] + sum_{l<L} beta_l[c,k] * dz_l[b,m,c]
- * `base` may be NULL (treated as zero).  `dz` and `beta` are host arrays of L
+ * `base` may be NULL (treated as zero) when L == 1 — the plain write.  `dz`
+ * and `beta` are host arrays of L
  * device pointers ([B,M,C] and [C,K]).  Accumulation: acc = base, then
  * acc = fma(beta_l, dz_l, acc) for l = 0..L-1, one rounding at the store.
  * Replaces

@@ -214,15 +214,26 @@ def test_edge_shapes_fp32(coracle, B, G, C, L):
     assert_f32(host(gam), coracle.Cgamma(d["alpha"], list(d["beta"])), tol=1e-6, what="gamma")
 
 
-def test_fp16_and_bf16_weights(coracle):
+@pytest.mark.parametrize("xdt,wdt", [(torch.float16, torch.float16), (torch.float16, F32), (BF16, BF16)])
+def test_16bit_activations_and_weights(coracle, xdt, wdt):
     d = cfg(2, 16, 768, 3)
-    x0 = dev(d["x0"], torch.float16)
-    betas = [dev(b, BF16) for b in d["beta"]]
-    dzs = [dev(z, torch.float16) for z in d["dz"]]
+    x0 = dev(d["x0"], xdt)
+    betas = [dev(b, wdt) for b in d["beta"]]
+    dzs = [dev(z, xdt) for z in d["dz"]]
     got = host(capi.materialise(x0, dzs, betas))
     ref = coracle.Cwrite(host(x0), [host(z) for z in dzs], [host(b) for b in betas])
+    ulp = 2.0**-11 if xdt == torch.float16 else 2.0**-8
     d_ = np.abs(got - ref)
-    assert (d_ <= 2.0**-11 * np.abs(ref) + 1e-6).all(), f"fp16 rounding bound violated: {d_.max()}"
+    assert (d_ <= ulp * np.abs(ref) + 1e-6).all(), f"rounding bound violated: {d_.max()}"
+    za = host(capi.read(x0, dev(d["alpha"], wdt)))
+    zr = coracle.Cread(host(x0), rounded(d["alpha"], wdt), 16)
+    assert (np.abs(za - zr) <= ulp * np.abs(zr) + 1e-5).all()
+    # a pair without compiled kernels (fp16 activations, bf16 weights) goes through the op, which widens the weights
+    if xdt == torch.float16:
+        bb = torch.stack(betas).to(BF16)
+        out = ops.final_accumulate_b4_traceable(x0, torch.stack(dzs), bb)
+        ref2 = coracle.Cwrite(host(x0), [host(z) for z in dzs], [host(b) for b in bb])
+        assert (np.abs(host(out) - ref2) <= ulp * np.abs(ref2) + 1e-6).all()
 
 
 def test_empty_batch_and_misaligned_inputs():
