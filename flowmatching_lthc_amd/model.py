@@ -1,0 +1,524 @@
+"""LTHC-B/4 shared-read model around the HIP interface.
+
+The workspace transformer, embedders and decoder are plain PyTorch (their
+GEMMs and attention run through hipBLASLt / the SDPA kernels of PyTorch-ROCm);
+the high-resolution interface -- shared read, lazy workspace recurrence and
+the single final materialisation -- runs through the ``jit_thc`` HIP ops.
+
+The module tree, parameter names, initialisation and forward math follow
+flowmatching_lthc/models/local_thc.py (SharedReadLocalTHCSharedAdaLNJiT,
+:1331-1394, its FusedFinal12 subclass :1413-1420 and the components at
+:84-323, :853-1007) and flowmatching_lthc/models/jit_shared_adaln.py
+(RMSNorm :20-30, VisionRotaryEmbeddingFast :33-59), so a reference state dict
+loads unchanged and ``build_model('lthc_b4_velocity')`` builds the same network.
+"""
+
+from __future__ import annotations
+
+import math
+import re
+from contextlib import nullcontext
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+from torch.nn.attention import SDPBackend, sdpa_kernel
+
+from . import ops
+from .local_thc import LayerLocalWrite, SharedLocalRead
+
+
+def modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """x * (1 + scale) + shift with per-sample [B, C] shift/scale (local_thc.py:37-38)."""
+    return x * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1)
+
+
+class RMSNorm(nn.Module):
+    """RMS normalisation computed in fp32, returned in the input dtype (jit_shared_adaln.py:20-30)."""
+
+    def __init__(self, dim: int, eps: float = 1e-6) -> None:
+        super().__init__()
+        self.weight = nn.Parameter(torch.ones(dim))
+        self.eps = eps
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        inv = torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return (xf * inv * self.weight).to(x.dtype)
+
+
+def _rotate_pairs(x: torch.Tensor) -> torch.Tensor:
+    """(x0, x1, x2, x3, ...) -> (-x1, x0, -x3, x2, ...): rotation of interleaved pairs."""
+    pairs = x.unflatten(-1, (-1, 2))
+    return torch.stack((-pairs[..., 1], pairs[..., 0]), dim=-1).flatten(-2)
+
+
+class VisionRotaryEmbeddingFast(nn.Module):
+    """2-D rotary embedding over a grid x grid token map (jit_shared_adaln.py:33-59).
+
+    A head of 2*dim channels rotates its first dim channels with the token's
+    row position and the last dim channels with its column position, in
+    interleaved (even, odd) pairs.
+    """
+
+    def __init__(self, dim: int, grid_size: int, num_prefix_tokens: int = 0, theta: float = 10000.0) -> None:
+        super().__init__()
+        inv = 1.0 / (theta ** (torch.arange(0, dim, 2).float()[: dim // 2] / dim))
+        pos = torch.arange(grid_size).float()
+        ang = torch.outer(pos, inv).repeat_interleave(2, dim=-1)  # [grid, dim]
+        rows = ang[:, None, :].expand(grid_size, grid_size, dim)
+        cols = ang[None, :, :].expand(grid_size, grid_size, dim)
+        table = torch.cat([rows, cols], dim=-1).reshape(grid_size * grid_size, 2 * dim)
+        cos, sin = table.cos(), table.sin()
+        if num_prefix_tokens:
+            cos = torch.cat([torch.ones(num_prefix_tokens, cos.shape[-1]), cos], dim=0)
+            sin = torch.cat([torch.zeros(num_prefix_tokens, sin.shape[-1]), sin], dim=0)
+        self.register_buffer("freqs_cos", cos, persistent=False)
+        self.register_buffer("freqs_sin", sin, persistent=False)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        cos = self.freqs_cos.to(x.device, x.dtype)
+        sin = self.freqs_sin.to(x.device, x.dtype)
+        return x * cos + _rotate_pairs(x) * sin
+
+
+class BottleneckPatchEmbedNHWC(nn.Module):
+    """Conv patchify (in -> bottleneck, kernel = stride = patch) then 1x1 conv to C, NHWC out (local_thc.py:64-89)."""
+
+    def __init__(
+        self,
+        img_size: int = 256,
+        patch_size: int = 4,
+        in_chans: int = 3,
+        bottleneck_dim: int = 128,
+        embed_dim: int = 768,
+        bias: bool = True,
+    ) -> None:
+        super().__init__()
+        self.img_size = (img_size, img_size)
+        self.patch_size = (patch_size, patch_size)
+        self.grid_size = (img_size // patch_size, img_size // patch_size)
+        self.num_patches = self.grid_size[0] * self.grid_size[1]
+        self.proj1 = nn.Conv2d(in_chans, bottleneck_dim, kernel_size=patch_size, stride=patch_size, bias=False)
+        self.proj2 = nn.Conv2d(bottleneck_dim, embed_dim, kernel_size=1, stride=1, bias=bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if tuple(x.shape[-2:]) != self.img_size:
+            raise ValueError(f"expected image size {self.img_size}, got {tuple(x.shape[-2:])}")
+        return self.proj2(self.proj1(x)).permute(0, 2, 3, 1).contiguous()
+
+
+class TimestepEmbedder(nn.Module):
+    """Sinusoidal timestep features (cos then sin) through a 2-layer SiLU MLP (local_thc.py:175-200)."""
+
+    def __init__(self, hidden_size: int, frequency_embedding_size: int = 256) -> None:
+        super().__init__()
+        self.frequency_embedding_size = frequency_embedding_size
+        self.mlp = nn.Sequential(
+            nn.Linear(frequency_embedding_size, hidden_size, bias=True),
+            nn.SiLU(),
+            nn.Linear(hidden_size, hidden_size, bias=True),
+        )
+
+    @staticmethod
+    def timestep_embedding(t: torch.Tensor, dim: int, max_period: int = 10000) -> torch.Tensor:
+        half = dim // 2
+        k = torch.arange(half, dtype=torch.float32, device=t.device)
+        freqs = torch.exp(-math.log(max_period) * k / half)
+        args = t.float()[:, None] * freqs[None]
+        emb = torch.cat([args.cos(), args.sin()], dim=-1)
+        if dim % 2:
+            emb = F.pad(emb, (0, 1))
+        return emb
+
+    def forward(self, t: torch.Tensor) -> torch.Tensor:
+        return self.mlp(self.timestep_embedding(t, self.frequency_embedding_size))
+
+
+class LabelEmbedder(nn.Module):
+    """num_classes + 1 embeddings (the last one is the null label used for guidance) (local_thc.py:203-210)."""
+
+    def __init__(self, num_classes: int, hidden_size: int) -> None:
+        super().__init__()
+        self.num_classes = num_classes
+        self.embedding_table = nn.Embedding(num_classes + 1, hidden_size)
+
+    def forward(self, labels: torch.Tensor) -> torch.Tensor:
+        return self.embedding_table(labels)
+
+
+class WorkspaceAttention(nn.Module):
+    """QK-RMSNorm multi-head self-attention with 2-D RoPE over the workspace tokens (local_thc.py:213-256)."""
+
+    def __init__(
+        self,
+        dim: int,
+        num_heads: int = 12,
+        qkv_bias: bool = True,
+        qk_norm: bool = True,
+        attn_drop: float = 0.0,
+        proj_drop: float = 0.0,
+        attn_backend: str = "flash",
+    ) -> None:
+        super().__init__()
+        if dim % num_heads != 0:
+            raise ValueError(f"dim={dim} must be divisible by num_heads={num_heads}")
+        self.num_heads = num_heads
+        self.head_dim = dim // num_heads
+        self.qkv = nn.Linear(dim, dim * 3, bias=qkv_bias)
+        self.q_norm = RMSNorm(self.head_dim) if qk_norm else nn.Identity()
+        self.k_norm = RMSNorm(self.head_dim) if qk_norm else nn.Identity()
+        self.attn_drop = nn.Dropout(attn_drop)
+        self.proj = nn.Linear(dim, dim)
+        self.proj_drop = nn.Dropout(proj_drop)
+        self.attn_backend = attn_backend
+
+    def _backends(self):
+        table = {
+            "flash": [SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION, SDPBackend.MATH],
+            "efficient": [SDPBackend.EFFICIENT_ATTENTION, SDPBackend.MATH],
+            "math": [SDPBackend.MATH],
+        }
+        return sdpa_kernel(table[self.attn_backend]) if self.attn_backend in table else nullcontext()
+
+    def forward(self, x: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> torch.Tensor:
+        b, n, c = x.shape
+        q, k, v = self.qkv(x).view(b, n, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
+        q = rope(self.q_norm(q))
+        k = rope(self.k_norm(k))
+        with self._backends():
+            o = F.scaled_dot_product_attention(q, k, v, dropout_p=self.attn_drop.p if self.training else 0.0)
+        return self.proj_drop(self.proj(o.transpose(1, 2).reshape(b, n, c)))
+
+
+class SwiGLUFFN(nn.Module):
+    """SwiGLU MLP with hidden width int(hidden_dim * 2 / 3); w12 output split (gate, value) (local_thc.py:259-269)."""
+
+    def __init__(self, dim: int, hidden_dim: int, drop: float = 0.0, bias: bool = True) -> None:
+        super().__init__()
+        hidden = int(hidden_dim * 2 / 3)
+        self.w12 = nn.Linear(dim, 2 * hidden, bias=bias)
+        self.w3 = nn.Linear(hidden, dim, bias=bias)
+        self.ffn_dropout = nn.Dropout(drop)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        gate, value = self.w12(x).chunk(2, dim=-1)
+        return self.w3(self.ffn_dropout(F.silu(gate) * value))
+
+
+class WorkspaceSharedAdaLNBranch(nn.Module):
+    """Attention + SwiGLU branch on the workspace, modulated by the shared [B, 6C] AdaLN vector (local_thc.py:302-323).
+
+    Returns the branch update dZ = gate_msa * attn(...) + gate_mlp * mlp(...).
+    """
+
+    def __init__(
+        self,
+        hidden_size: int,
+        num_heads: int,
+        mlp_ratio: float = 4.0,
+        attn_drop: float = 0.0,
+        proj_drop: float = 0.0,
+        attn_backend: str = "flash",
+    ) -> None:
+        super().__init__()
+        self.norm1 = RMSNorm(hidden_size, eps=1e-6)
+        self.attn = WorkspaceAttention(hidden_size, num_heads, attn_drop=attn_drop, proj_drop=proj_drop, attn_backend=attn_backend)
+        self.norm2 = RMSNorm(hidden_size, eps=1e-6)
+        self.mlp = SwiGLUFFN(hidden_size, int(hidden_size * mlp_ratio), drop=proj_drop)
+
+    def forward(self, z: torch.Tensor, t6: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> torch.Tensor:
+        sh_a, sc_a, g_a, sh_m, sc_m, g_m = t6.chunk(6, dim=-1)
+        d_attn = g_a.unsqueeze(1) * self.attn(modulate(self.norm1(z), sh_a, sc_a), rope)
+        d_mlp = g_m.unsqueeze(1) * self.mlp(modulate(self.norm2(z + d_attn), sh_m, sc_m))
+        return d_attn + d_mlp
+
+
+class FinalLayerSharedAdaLN(nn.Module):
+    """RMSNorm, shared [B, 2C] modulation (shift, scale), linear to patch pixels (local_thc.py:865-873)."""
+
+    def __init__(self, hidden_size: int, patch_size: int, out_channels: int) -> None:
+        super().__init__()
+        self.norm_final = RMSNorm(hidden_size)
+        self.linear = nn.Linear(hidden_size, patch_size * patch_size * out_channels, bias=True)
+
+    def forward(self, x: torch.Tensor, t2: torch.Tensor) -> torch.Tensor:
+        shift, scale = t2.chunk(2, dim=1)
+        return self.linear(modulate(self.norm_final(x), shift, scale))
+
+
+class SharedReadLocalTHCSharedAdaLNJiTBlock(nn.Module):
+    """One layer: the layer's local write and its workspace branch (local_thc.py:1286-1328)."""
+
+    def __init__(
+        self,
+        hidden_size: int,
+        num_heads: int,
+        high_grid: int,
+        workspace_grid: int = 16,
+        pool_groups: int | None = None,
+        mlp_ratio: float = 4.0,
+        attn_drop: float = 0.0,
+        proj_drop: float = 0.0,
+        attn_backend: str = "flash",
+    ) -> None:
+        super().__init__()
+        pool_groups = hidden_size if pool_groups is None else pool_groups
+        self.write = LayerLocalWrite(high_grid, workspace_grid, hidden_size, pool_groups)
+        self.branch = WorkspaceSharedAdaLNBranch(hidden_size, num_heads, mlp_ratio, attn_drop, proj_drop, attn_backend)
+
+    @property
+    def read(self) -> LayerLocalWrite:
+        """Old checkpoint name of the layer's write module."""
+        return self.write
+
+    def forward_naive(self, x_hi, t6, rope, shared_read: SharedLocalRead) -> torch.Tensor:
+        z = shared_read.read(x_hi)
+        return self.write.write_add(x_hi, self.branch(z, t6, rope))
+
+    def branch_update(self, z: torch.Tensor, t6: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> torch.Tensor:
+        return self.branch(z, t6, rope)
+
+    def lazy_workspace_update(self, z: torch.Tensor, dz: torch.Tensor, shared_read: SharedLocalRead) -> torch.Tensor:
+        """Z_{l+1} = Z_l + gamma_l * dZ_l; gamma_l from the shared read and this layer's write weights."""
+        gamma = self.write.gamma_from_alpha(shared_read.alpha(dtype=dz.dtype))
+        return ops.lazy_workspace_update(z, dz, gamma)
+
+
+def migrate_lthc_state_dict_keys(state_dict: dict) -> dict:
+    """Old checkpoint key names -> current ones (local_thc.py:41-61): the old code called the read 'write'."""
+    rules = (
+        (r"shared_write\.", "shared_read."),
+        (r"blocks\.(\d+)\.read\.", r"blocks.\1.write."),
+        (r"\.write_logits", ".read_logits"),
+        (r"\.read_weight", ".write_weight"),
+    )
+    out = {}
+    for key, value in state_dict.items():
+        for pat, rep in rules:
+            key = re.sub(pat, rep, key)
+        out[key] = value
+    return out
+
+
+class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
+    """LTHC JiT with a depth-shared read, per-layer writes and shared AdaLN (local_thc.py:883-1007, :1331-1394).
+
+    forward_lazy: read X0 once, run the blocks on the workspace with the exact
+    recurrence Z_{l+1} = Z_l + gamma_l dZ_l, materialise X_L once, decode.
+    forward_naive: per block read X_l, branch, write back X_{l+1} = X_l + P_l dZ_l.
+    """
+
+    block_cls = SharedReadLocalTHCSharedAdaLNJiTBlock
+
+    def __init__(
+        self,
+        input_size: int = 256,
+        patch_size: int = 4,
+        in_channels: int = 3,
+        hidden_size: int = 768,
+        depth: int = 12,
+        num_heads: int = 12,
+        mlp_ratio: float = 4.0,
+        attn_drop: float = 0.0,
+        proj_drop: float = 0.0,
+        num_classes: int = 1000,
+        bottleneck_dim: int = 128,
+        workspace_grid: int = 16,
+        pool_groups: int | None = None,
+        attn_backend: str = "flash",
+        use_lazy: bool = True,
+    ) -> None:
+        super().__init__()
+        high_grid = input_size // patch_size
+        if high_grid % workspace_grid != 0:
+            raise ValueError(f"input_size/patch_size={high_grid} must be divisible by workspace_grid={workspace_grid}")
+        self.input_size = input_size
+        self.patch_size = patch_size
+        self.in_channels = in_channels
+        self.out_channels = in_channels
+        self.hidden_size = hidden_size
+        self.depth = depth
+        self.num_heads = num_heads
+        self.num_classes = num_classes
+        self.workspace_grid = workspace_grid
+        self.high_grid = high_grid
+        self.num_high_tokens = high_grid * high_grid
+        self.num_workspace_tokens = workspace_grid * workspace_grid
+        self.pool_groups = hidden_size if pool_groups is None else pool_groups
+
+        self.t_embedder = TimestepEmbedder(hidden_size)
+        self.y_embedder = LabelEmbedder(num_classes, hidden_size)
+        self.x_embedder = BottleneckPatchEmbedNHWC(input_size, patch_size, in_channels, bottleneck_dim, hidden_size)
+        self.workspace_rope = VisionRotaryEmbeddingFast(hidden_size // num_heads // 2, workspace_grid)
+        quarter = depth // 4
+        self.blocks = nn.ModuleList(
+            self.block_cls(
+                hidden_size=hidden_size,
+                num_heads=num_heads,
+                high_grid=high_grid,
+                workspace_grid=workspace_grid,
+                pool_groups=self.pool_groups,
+                mlp_ratio=mlp_ratio,
+                attn_drop=attn_drop if quarter <= i < 3 * quarter else 0.0,
+                proj_drop=proj_drop if quarter <= i < 3 * quarter else 0.0,
+                attn_backend=attn_backend,
+            )
+            for i in range(depth)
+        )
+        self.final_layer = FinalLayerSharedAdaLN(hidden_size, patch_size, self.out_channels)
+        self.shared_adaLN_modulation = nn.Sequential(nn.SiLU(), nn.Linear(hidden_size, 6 * hidden_size, bias=True))
+        self.shared_final_modulation = nn.Sequential(nn.SiLU(), nn.Linear(hidden_size, 2 * hidden_size, bias=True))
+        self.initialize_weights()
+        self.shared_read = SharedLocalRead(high_grid, workspace_grid, hidden_size, self.pool_groups, use_softmax_write=True)
+        self.use_lazy = bool(use_lazy)
+
+    # -- initialisation (local_thc.py:944-970, :1004-1007) ------------------------------------------
+    def initialize_weights(self) -> None:
+        for m in self.modules():
+            if isinstance(m, nn.Linear):
+                nn.init.xavier_uniform_(m.weight)
+                if m.bias is not None:
+                    nn.init.zeros_(m.bias)
+        for conv in (self.x_embedder.proj1, self.x_embedder.proj2):
+            nn.init.xavier_uniform_(conv.weight.data.view(conv.weight.shape[0], -1))
+        nn.init.zeros_(self.x_embedder.proj2.bias)
+        nn.init.normal_(self.y_embedder.embedding_table.weight, std=0.02)
+        nn.init.normal_(self.t_embedder.mlp[0].weight, std=0.02)
+        nn.init.normal_(self.t_embedder.mlp[2].weight, std=0.02)
+        nn.init.zeros_(self.final_layer.linear.weight)
+        nn.init.zeros_(self.final_layer.linear.bias)
+        for head in (self.shared_adaLN_modulation[-1], self.shared_final_modulation[-1]):
+            nn.init.zeros_(head.weight)
+            nn.init.zeros_(head.bias)
+
+    def load_state_dict(self, state_dict, strict: bool = True, assign: bool = False):
+        return super().load_state_dict(migrate_lthc_state_dict_keys(state_dict), strict=strict, assign=assign)
+
+    @property
+    def shared_write(self) -> SharedLocalRead:
+        """Old name of the shared read."""
+        return self.shared_read
+
+    def unpatchify(self, x: torch.Tensor) -> torch.Tensor:
+        """[B, h*w, p*p*c] -> [B, c, h*p, w*p] (local_thc.py:972-980)."""
+        c, p = self.out_channels, self.patch_size
+        h = w = math.isqrt(x.shape[1])
+        if h * w != x.shape[1]:
+            raise ValueError(f"token count {x.shape[1]} is not square")
+        x = x.reshape(x.shape[0], h, w, p, p, c).permute(0, 5, 1, 3, 2, 4)
+        return x.reshape(x.shape[0], c, h * p, w * p)
+
+    # -- interface ---------------------------------------------------------------------------------
+    def final_accumulate_reference(self, x0: torch.Tensor, dz_list: list[torch.Tensor]) -> torch.Tensor:
+        """X_L = X0 + sum_l P_l(dZ_l) in one pass (the reference's generic loop, local_thc.py:1368-1372)."""
+        if len(dz_list) != len(self.blocks):
+            raise ValueError(f"expected {len(self.blocks)} updates, got {len(dz_list)}")
+        betas = torch.stack([blk.write.channel_beta(dtype=torch.float32) for blk in self.blocks])
+        return ops.final_accumulate_b4_traceable(x0, torch.stack(dz_list), betas)
+
+    def _conditioning(self, t: torch.Tensor, y: torch.Tensor):
+        c = self.t_embedder(t) + self.y_embedder(y)
+        return self.shared_adaLN_modulation(c), self.shared_final_modulation(c)
+
+    def _decode(self, x_hi: torch.Tensor, t2: torch.Tensor) -> torch.Tensor:
+        b, hh, wh, c_dim = x_hi.shape
+        return self.unpatchify(self.final_layer(x_hi.reshape(b, hh * wh, c_dim), t2))
+
+    def forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+        t6, t2 = self._conditioning(t, y)
+        x0 = self.x_embedder(x)
+        z = self.shared_read.read(x0)
+        dz_list = []
+        for block in self.blocks:
+            dz = block.branch_update(z, t6, self.workspace_rope)
+            dz_list.append(dz)
+            z = block.lazy_workspace_update(z, dz, self.shared_read)
+        return self._decode(self.final_accumulate_reference(x0, dz_list), t2)
+
+    def forward_naive(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+        t6, t2 = self._conditioning(t, y)
+        x_hi = self.x_embedder(x)
+        for block in self.blocks:
+            x_hi = block.forward_naive(x_hi, t6, self.workspace_rope, self.shared_read)
+        return self._decode(x_hi, t2)
+
+    def forward(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor, use_lazy: bool | None = None) -> torch.Tensor:
+        lazy = self.use_lazy if use_lazy is None else use_lazy
+        return self.forward_lazy(x, t, y) if lazy else self.forward_naive(x, t, y)
+
+
+class SharedReadFusedFinal12LocalTHCSharedAdaLNJiT(SharedReadLocalTHCSharedAdaLNJiT):
+    """Depth-12 form whose materialisation is the 12-pointer op (local_thc.py:1413-1420)."""
+
+    def final_accumulate_reference(self, x0: torch.Tensor, dz_list: list[torch.Tensor]) -> torch.Tensor:
+        if len(dz_list) != 12 or len(self.blocks) != 12:
+            raise ValueError("SharedReadFusedFinal12LocalTHCSharedAdaLNJiT requires depth=12")
+        betas = [blk.write.channel_beta() for blk in self.blocks]
+        return ops.final_accumulate_b4_12_traceable(x0, *dz_list, *betas)
+
+
+# Old class names (local_thc.py:1428-1431).
+SharedWriteLocalTHCSharedAdaLNJiTBlock = SharedReadLocalTHCSharedAdaLNJiTBlock
+SharedWriteLocalTHCSharedAdaLNJiT = SharedReadLocalTHCSharedAdaLNJiT
+SharedWriteFusedFinal12LocalTHCSharedAdaLNJiT = SharedReadFusedFinal12LocalTHCSharedAdaLNJiT
+
+
+def SharedRead_FusedFinal12_LocalTHC_SharedAdaLN_JiT_B_4(**kwargs) -> SharedReadFusedFinal12LocalTHCSharedAdaLNJiT:
+    """LTHC-B/4: patch 4, hidden 768, depth 12, 12 heads, bottleneck 128, 16x16 workspace (local_thc.py:1705-1719)."""
+    kwargs.setdefault("pool_groups", 768)
+    return SharedReadFusedFinal12LocalTHCSharedAdaLNJiT(
+        patch_size=4, hidden_size=768, depth=12, num_heads=12, bottleneck_dim=128, workspace_grid=16, **kwargs
+    )
+
+
+def SharedRead_LocalTHC_SharedAdaLN_JiT_B_4(**kwargs) -> SharedReadLocalTHCSharedAdaLNJiT:
+    kwargs.setdefault("pool_groups", 768)
+    return SharedReadLocalTHCSharedAdaLNJiT(
+        patch_size=4, hidden_size=768, depth=12, num_heads=12, bottleneck_dim=128, workspace_grid=16, **kwargs
+    )
+
+
+LocalTHC_JiT_models = {
+    "SharedRead-FusedFinal12-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_FusedFinal12_LocalTHC_SharedAdaLN_JiT_B_4,
+    "SharedWrite-FusedFinal12-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_FusedFinal12_LocalTHC_SharedAdaLN_JiT_B_4,
+    "SharedRead-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_LocalTHC_SharedAdaLN_JiT_B_4,
+    "SharedWrite-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_LocalTHC_SharedAdaLN_JiT_B_4,
+}
+
+MODEL_NAMES = (
+    "lthc_b4_velocity",
+    "local_thc_jit_shared_read_fused_final12_shared_adaln_b4",
+    "local_thc_jit_shared_write_fused_final12_shared_adaln_b4",
+)
+
+
+def build_model(name: str = "lthc_b4_velocity", **kwargs) -> nn.Module:
+    """The released LTHC-B/4 shared-read fused-final12 model (flowmatching_lthc/models/__init__.py:17-28)."""
+    if name in MODEL_NAMES:
+        return LocalTHC_JiT_models["SharedRead-FusedFinal12-LocalTHC-SharedAdaLN-JiT-B/4"](**kwargs)
+    if name in LocalTHC_JiT_models:
+        return LocalTHC_JiT_models[name](**kwargs)
+    raise ValueError(f"unknown model: {name}; available={MODEL_NAMES + tuple(LocalTHC_JiT_models)}")
+
+
+@torch.no_grad()
+def randomize_parameters(model: nn.Module, seed: int = 0, std: float = 0.02) -> nn.Module:
+    """Re-draw every parameter (the default init zeroes the AdaLN heads and the decoder, making the output 0).
+
+    Norm weights are drawn around 1 and the read logits around 0; everything
+    else is N(0, std^2).  The draw uses one CPU generator in parameter order.
+    """
+    gen = torch.Generator().manual_seed(seed)
+    for name, p in model.named_parameters():
+        r = torch.randn(p.shape, generator=gen)
+        if "norm" in name.split(".")[-2]:
+            r = 1.0 + 0.1 * r
+        elif name.endswith("write_weight"):
+            r = 1.0 + 0.5 * r
+        elif name.endswith("read_logits"):
+            r = 0.5 * r
+        else:
+            r = std * r
+        p.copy_(r.to(p.device, p.dtype))
+    return model

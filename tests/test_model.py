@@ -1,0 +1,153 @@
+"""Full LTHC model: structure and transformer parity on the CPU (no HIP op runs here).
+
+The golden fixture tests/golden/lthc_tiny_model.pt holds the reference model's
+outputs on a tiny configuration (written by tests/golden/make_model_fixture.py).
+On the CPU the interface hooks are supplied by library convolutions
+(depthwise conv2d / conv_transpose2d, the equivalences the reference states at
+local_thc.py:620-692), so these tests pin the restated transformer, embedders
+and decoder; tests/test_gpu_model.py runs the same fixture through the HIP ops.
+"""
+
+import os
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from flowmatching_lthc_amd import model as M
+
+FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "lthc_tiny_model.pt")
+CONFIG = dict(input_size=32, patch_size=4, hidden_size=32, depth=2, num_heads=2, num_classes=10, bottleneck_dim=8, workspace_grid=2, attn_backend="math")
+
+
+def load_fixture():
+    return torch.load(FIXTURE, weights_only=True)
+
+
+def conv_interface(model, form="conv"):
+    """Replace the HIP interface hooks with torch forms of the same maps.
+
+    form="conv": depthwise conv2d / conv_transpose2d (library routines, used on the CPU);
+    form="reshape": the cell view [B,G,4,G,4,C] times the weights (no MIOpen search, used on the GPU).
+    """
+    s = model.high_grid // model.workspace_grid
+    c = model.hidden_size
+    g = model.workspace_grid
+
+    def read(x):
+        a = model.shared_read.alpha(dtype=x.dtype)
+        if form == "conv":
+            z = F.conv2d(x.permute(0, 3, 1, 2), a.reshape(c, 1, s, s), stride=s, groups=c)
+            return z.permute(0, 2, 3, 1).reshape(x.shape[0], -1, c)
+        cells = x.reshape(x.shape[0], g, s, g, s, c).permute(0, 1, 3, 2, 4, 5).reshape(x.shape[0], g * g, s * s, c)
+        return (cells * a.t()[None, None]).sum(2)
+
+    def write(dz, w):
+        if form == "conv":
+            out = F.conv_transpose2d(dz.reshape(dz.shape[0], g, g, c).permute(0, 3, 1, 2), w.reshape(c, 1, s, s), stride=s, groups=c)
+            return out.permute(0, 2, 3, 1)
+        cells = dz[:, :, None, :] * w.t()[None, None]
+        return cells.reshape(dz.shape[0], g, g, s, s, c).permute(0, 1, 3, 2, 4, 5).reshape(dz.shape[0], g * s, g * s, c)
+
+    model.shared_read.read = read
+    for blk in model.blocks:
+        blk.write.write_add = lambda x_hi, dz, b=blk: x_hi + write(dz, b.write.beta(dtype=dz.dtype))
+
+        def lazy(z, dz, shared_read, b=blk):
+            return z + b.write.gamma_from_alpha(shared_read.alpha(dtype=dz.dtype))[None, None, :] * dz
+
+        blk.lazy_workspace_update = lazy
+
+    def final(x0, dz_list):
+        x = x0
+        for blk, dz in zip(model.blocks, dz_list, strict=True):
+            x = x + write(dz, blk.write.beta(dtype=dz.dtype))
+        return x
+
+    model.final_accumulate_reference = final
+    return model
+
+
+def rel(a, b):
+    return float((a - b).abs().max() / b.abs().max())
+
+
+def test_fixture_loads_safely_and_keys_match():
+    fx = load_fixture()
+    ours = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG)
+    sd = ours.state_dict()
+    assert set(sd) == set(fx["state_dict"])
+    for k, v in fx["state_dict"].items():
+        assert sd[k].shape == v.shape, k
+    ours.load_state_dict(fx["state_dict"])
+
+
+def test_transformer_matches_reference_fixture_on_cpu():
+    fx = load_fixture()
+    ours = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG).eval()
+    ours.load_state_dict(fx["state_dict"])
+    conv_interface(ours)
+    with torch.no_grad():
+        x0 = ours.x_embedder(fx["x"])
+        assert rel(x0, fx["x0"]) <= 1e-6
+        assert rel(ours.shared_read.read(x0), fx["z0"]) <= 1e-6
+        assert rel(ours(fx["x"], fx["t"], fx["y"], use_lazy=True), fx["out_lazy"]) <= 1e-5
+        assert rel(ours(fx["x"], fx["t"], fx["y"], use_lazy=False), fx["out_naive"]) <= 1e-5
+
+
+def test_reshape_form_equals_conv_form():
+    """The GPU tests' torch reference (cell reshape) is pinned to the library convolutions here."""
+    fx = load_fixture()
+    a = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG).eval()
+    a.load_state_dict(fx["state_dict"])
+    b = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG).eval()
+    b.load_state_dict(fx["state_dict"])
+    conv_interface(a, "conv")
+    conv_interface(b, "reshape")
+    with torch.no_grad():
+        for lazy in (True, False):
+            assert rel(b(fx["x"], fx["t"], fx["y"], use_lazy=lazy), a(fx["x"], fx["t"], fx["y"], use_lazy=lazy)) <= 1e-5
+
+
+def test_mutated_rope_layout_is_caught():
+    """Transposing the token grid of the RoPE table (rows for columns) must break fixture parity."""
+    fx = load_fixture()
+    ours = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG).eval()
+    ours.load_state_dict(fx["state_dict"])
+    conv_interface(ours)
+    rope = ours.workspace_rope
+    g = ours.workspace_grid
+    perm = torch.arange(g * g).reshape(g, g).t().reshape(-1)
+    rope.freqs_cos = rope.freqs_cos[perm]
+    rope.freqs_sin = rope.freqs_sin[perm]
+    with torch.no_grad():
+        out = ours(fx["x"], fx["t"], fx["y"], use_lazy=True)
+    assert rel(out, fx["out_lazy"]) > 1e-3
+
+
+def test_released_model_shape_and_names():
+    m = M.build_model("lthc_b4_velocity")
+    assert sum(p.numel() for p in m.parameters()) == 91_633_968  # README.md:138 (91.63 M)
+    names = dict(m.named_parameters())
+    assert names["shared_read.read_logits"].shape == (768, 16)
+    for i in range(12):
+        assert names[f"blocks.{i}.write.write_weight"].shape == (768, 16)
+    assert isinstance(m, M.SharedReadFusedFinal12LocalTHCSharedAdaLNJiT)
+    with pytest.raises(ValueError, match="unknown model"):
+        M.build_model("nope")
+
+
+def test_legacy_checkpoint_keys_migrate():
+    old = {
+        "shared_write.write_logits": torch.zeros(768, 16),
+        "blocks.3.read.read_weight": torch.ones(768, 16),
+        "blocks.3.branch.norm1.weight": torch.ones(768),
+    }
+    new = M.migrate_lthc_state_dict_keys(old)
+    assert set(new) == {"shared_read.read_logits", "blocks.3.write.write_weight", "blocks.3.branch.norm1.weight"}
+
+
+def test_wrong_image_size_raises():
+    m = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG)
+    with pytest.raises(ValueError, match="expected image size"):
+        m.x_embedder(torch.zeros(1, 3, 16, 16))
