@@ -48,6 +48,9 @@ def parse_args():
     p.add_argument("--mode", choices=["graph", "eager"], default="graph", help="how `value` is timed")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--model-batch", type=int, default=64, help="batch of the LTHC-B/4 forward leg (fwd img/s)")
+    p.add_argument("--model-steps", type=int, default=10)
+    p.add_argument("--no-model", action="store_true", help="skip the LTHC-B/4 forward leg")
     p.add_argument(
         "--profile",
         choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy"],
@@ -118,6 +121,79 @@ def cpu_baseline(G, C, L, budget_s):
             f"{dt * n:.1f} s; value = the bf16 algorithmic bytes of that slice / time per step"
         ),
         "ms_per_step_sample": round(dt * 1e3, 3),
+    }
+
+
+def eager_interface(model, torch):
+    """The reference's PyTorch op sequence for the interface hooks (local_thc.py:1211-1223 read as a broadcast
+    multiply + sum, local_thc.py:1325-1328 recurrence, local_thc.py:1368-1372 materialise as a write_add loop)."""
+    g, c = model.workspace_grid, model.hidden_size
+
+    def read(x):
+        a = model.shared_read.alpha(dtype=x.dtype)
+        cells = x.reshape(x.shape[0], g, 4, g, 4, c).permute(0, 1, 3, 2, 4, 5).reshape(x.shape[0], g * g, 16, c)
+        return (cells * a.t()[None, None]).sum(2)
+
+    def write(dz, w):
+        cells = dz[:, :, None, :] * w.t()[None, None]
+        return cells.reshape(dz.shape[0], g, g, 4, 4, c).permute(0, 1, 3, 2, 4, 5).reshape(dz.shape[0], 4 * g, 4 * g, c)
+
+    model.shared_read.read = read
+    for blk in model.blocks:
+        blk.lazy_workspace_update = lambda z, dz, sr, b=blk: z + b.write.gamma_from_alpha(sr.alpha(dtype=dz.dtype))[None, None, :] * dz
+
+    def final(x0, dz_list):
+        x = x0
+        for blk, dz in zip(model.blocks, dz_list):
+            x = x + write(dz, blk.write.beta(dtype=dz.dtype))
+        return x
+
+    model.final_accumulate_reference = final
+    return model
+
+
+def model_forward(args, torch, dev):
+    """LTHC-B/4 forward, random-init weights, bf16 autocast, images [B,3,256,256] ~ N(0,1), t ~ U(0,1), labels
+    uniform in [0,1000).  Timed with the HIP interface and, for comparison, with the interface as torch eager ops."""
+    from flowmatching_lthc_amd import model as M
+
+    B = args.model_batch
+    gen = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn((B, 3, 256, 256), generator=gen, device=dev)
+    t = torch.rand((B,), generator=gen, device=dev)
+    y = torch.randint(0, 1000, (B,), generator=gen, device=dev)
+    stream = torch.cuda.current_stream()
+
+    def timed(m):
+        def fwd():
+            with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+                return m(x, t, y)
+
+        for _ in range(args.warmup):
+            fwd()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.model_steps):
+            out = fwd()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.model_steps, out
+
+    ours = M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=0).to(dev).eval()
+    ms, out_ours = timed(ours)
+    eager = eager_interface(M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=0).to(dev).eval(), torch)
+    ms_eager, out_eager = timed(eager)
+    diff = float((out_ours.float() - out_eager.float()).abs().max() / out_eager.float().abs().max())
+    return {
+        "img_per_s": round(B / (ms * 1e-3), 1),
+        "ms_per_fwd": round(ms, 4),
+        "batch": B,
+        "steps": args.model_steps,
+        "workload": "LTHC-B/4 velocity forward (lthc_b4_velocity), random-init weights, bf16 autocast, eager",
+        "torch_eager_interface_img_per_s": round(B / (ms_eager * 1e-3), 1),
+        "torch_eager_interface_ms_per_fwd": round(ms_eager, 4),
+        "max_rel_diff_vs_torch_eager_interface": diff,
     }
 
 
@@ -258,6 +334,10 @@ def main():
     mat_achieved = nbytes["materialise"] / (mat_ms * 1e-3)
     traffic = pmc_traffic()
 
+    del sets, graphs
+    torch.cuda.empty_cache()
+    model_fwd = None if args.no_model else model_forward(args, torch, dev)
+
     cpu = None
     if not args.no_cpu_baseline:
         cpu = cpu_baseline(G, C, L, args.cpu_seconds)
@@ -300,6 +380,7 @@ def main():
             "avg_launch_ms": round(mat_ms, 4),
         },
         "cpu_baseline": cpu,
+        "model_fwd": model_fwd,
         "extra": {
             "eager_ms_per_step": round(eager_ms, 4),
             "graph_ms_per_step": None if graph_ms is None else round(graph_ms, 4),

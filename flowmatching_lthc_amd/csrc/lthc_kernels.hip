@@ -24,6 +24,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <numeric>
 #include <string>
 #include <type_traits>
 
@@ -80,11 +81,20 @@ LTHC_DEV uint32_t pack2(float a, float b) {
   }
 }
 
-// Raw storage of N consecutive elements of format DT (N * bytes >= 4).
+// Narrowing of one value to a 16-bit format (round to nearest even), bits in the low half.
+template <int DT>
+LTHC_DEV uint32_t narrow1(float v) {
+  if constexpr (DT == LTHC_BF16) return __builtin_bit_cast(uint16_t, static_cast<__bf16>(v));
+  else return __builtin_bit_cast(uint16_t, static_cast<_Float16>(v));
+}
+
+// Raw storage of N consecutive elements of format DT: whole dwords, or one
+// 16-bit element (kBytes == 2, held in the low half of w[0]).
 template <int DT, int N>
 struct Raw {
-  static constexpr int kWords = N * Fmt<DT>::bytes / 4;
-  static_assert(kWords >= 1 && (kWords <= 2 || kWords % 4 == 0), "raw vector width");
+  static constexpr int kBytes = N * Fmt<DT>::bytes;
+  static constexpr int kWords = kBytes >= 4 ? kBytes / 4 : 1;
+  static_assert(kBytes == 2 || kWords <= 2 || kWords % 4 == 0, "raw vector width");
   uint32_t w[kWords];
 };
 
@@ -96,7 +106,9 @@ template <int DT, int N, bool NT = false, typename Off = int64_t>
 LTHC_DEV void load_at(const void* __restrict__ base, Off boff, Raw<DT, N>& r) {
   constexpr int W = Raw<DT, N>::kWords;
   const char* q = static_cast<const char*>(base) + boff;
-  if constexpr (W == 1) {
+  if constexpr (Raw<DT, N>::kBytes == 2) {
+    r.w[0] = NT ? __builtin_nontemporal_load(reinterpret_cast<const uint16_t*>(q)) : *reinterpret_cast<const uint16_t*>(q);
+  } else if constexpr (W == 1) {
     r.w[0] = NT ? __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(q)) : *reinterpret_cast<const uint32_t*>(q);
   } else if constexpr (W == 2) {
     const u32x2_t t = NT ? __builtin_nontemporal_load(reinterpret_cast<const u32x2_t*>(q)) : *reinterpret_cast<const u32x2_t*>(q);
@@ -126,6 +138,8 @@ LTHC_DEV void unpack_raw(const Raw<DT, N>& r, float (&v)[N]) {
   if constexpr (DT == LTHC_F32) {
 #pragma unroll
     for (int j = 0; j < N; ++j) v[j] = __uint_as_float(r.w[j]);
+  } else if constexpr (N == 1) {
+    v[0] = widen1<DT>(r.w[0]);
   } else {
 #pragma unroll
     for (int j = 0; j < N / 2; ++j) unpack2<DT>(r.w[j], v[2 * j], v[2 * j + 1]);
@@ -141,30 +155,36 @@ LTHC_DEV void load_vec(const void* __restrict__ p, int64_t i, float (&v)[N]) {
 
 template <int DT, int N, bool NT = false, typename Off = int64_t>
 LTHC_DEV void store_at(void* __restrict__ base, Off boff, const float (&v)[N]) {
-  constexpr int W = N * Fmt<DT>::bytes / 4;
-  uint32_t w[W];
-  if constexpr (DT == LTHC_F32) {
-#pragma unroll
-    for (int j = 0; j < N; ++j) w[j] = __float_as_uint(v[j]);
-  } else {
-#pragma unroll
-    for (int j = 0; j < N / 2; ++j) w[j] = pack2<DT>(v[2 * j], v[2 * j + 1]);
-  }
   char* q = static_cast<char*>(base) + boff;
-  if constexpr (W == 1) {
-    if (NT) __builtin_nontemporal_store(w[0], reinterpret_cast<uint32_t*>(q));
-    else *reinterpret_cast<uint32_t*>(q) = w[0];
-  } else if constexpr (W == 2) {
-    const u32x2_t t = {w[0], w[1]};
-    if (NT) __builtin_nontemporal_store(t, reinterpret_cast<u32x2_t*>(q));
-    else *reinterpret_cast<u32x2_t*>(q) = t;
+  if constexpr (N * Fmt<DT>::bytes == 2) {
+    const uint16_t h = static_cast<uint16_t>(narrow1<DT>(v[0]));
+    if (NT) __builtin_nontemporal_store(h, reinterpret_cast<uint16_t*>(q));
+    else *reinterpret_cast<uint16_t*>(q) = h;
   } else {
-    static_assert(W % 4 == 0, "store width");
+    constexpr int W = N * Fmt<DT>::bytes / 4;
+    uint32_t w[W];
+    if constexpr (DT == LTHC_F32) {
 #pragma unroll
-    for (int j = 0; j < W / 4; ++j) {
-      const u32x4_t t = {w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
-      if (NT) __builtin_nontemporal_store(t, reinterpret_cast<u32x4_t*>(q) + j);
-      else reinterpret_cast<u32x4_t*>(q)[j] = t;
+      for (int j = 0; j < N; ++j) w[j] = __float_as_uint(v[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < N / 2; ++j) w[j] = pack2<DT>(v[2 * j], v[2 * j + 1]);
+    }
+    if constexpr (W == 1) {
+      if (NT) __builtin_nontemporal_store(w[0], reinterpret_cast<uint32_t*>(q));
+      else *reinterpret_cast<uint32_t*>(q) = w[0];
+    } else if constexpr (W == 2) {
+      const u32x2_t t = {w[0], w[1]};
+      if (NT) __builtin_nontemporal_store(t, reinterpret_cast<u32x2_t*>(q));
+      else *reinterpret_cast<u32x2_t*>(q) = t;
+    } else {
+      static_assert(W % 4 == 0, "store width");
+#pragma unroll
+      for (int j = 0; j < W / 4; ++j) {
+        const u32x4_t t = {w[4 * j], w[4 * j + 1], w[4 * j + 2], w[4 * j + 3]};
+        if (NT) __builtin_nontemporal_store(t, reinterpret_cast<u32x4_t*>(q) + j);
+        else reinterpret_cast<u32x4_t*>(q)[j] = t;
+      }
     }
   }
 }
@@ -240,41 +260,50 @@ struct CellWalk {
 
 #define LTHC_PHASE_BARRIER() __builtin_amdgcn_sched_barrier(0)
 
+// Byte offset of tap (0, 0), channel 0 of a cell in the NHWC tensor: cell row
+// r = cell / G starts 4 high-res rows (4*H*C elements) after row r - 1, and
+// cell gx = cell % G starts 4*C elements into its tap row.
+LTHC_DEV int64_t cell_hoff(int64_t cell, int G, int C) {
+  const int64_t r = cell / G;
+  return (r * (kS * kS) * G + (cell - r * G) * kS) * C;
+}
+
 // ---------------------------------------------------------------------------
 // READ: z[cell, c] = sum_k alpha[c,k] x[cell, k, c]
 // Thread = VEC channels of one cell, all 16 taps; alpha for those channels
-// lives in VGPRs.  Block = cpi cells x ncv_blk channel vectors; each thread
-// walks every cpi-th cell of the block's range.  Off is the byte-offset type
-// (uint32_t when x is smaller than 4 GiB).
+// lives in VGPRs.  Block = cpi cells x ncv_blk channel vectors.  Cells are
+// visited grid-stride: the grid covers S = gridDim.x * cpi consecutive cells
+// at a time (a compact window of the tensor, which HBM serves faster than
+// one independent stream per block), and S % G == 0 makes every thread's
+// byte offsets advance by constants.  Off is the byte-offset type (uint32_t
+// when x is smaller than 4 GiB).
 // Accumulation order k = 0..15 (local_thc_triton_kernels.py:51-55).
 // ---------------------------------------------------------------------------
 template <int DT, int WDT, int VEC, typename Off>
 __global__ __launch_bounds__(kBlock) void read_fwd_kernel(const void* __restrict__ x, const void* __restrict__ w,
                                                           void* __restrict__ z, int64_t ncells, int G, int C,
-                                                          int ncv_blk, int cpi, int64_t cpb) {
+                                                          int ncv_blk, int cpi) {
   constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int ci = t / ncv_blk;
   const int c0 = (blockIdx.y * ncv_blk + (t - ci * ncv_blk)) * VEC;
-  if (ci >= cpi || c0 >= C) return;
+  int64_t cell = static_cast<int64_t>(blockIdx.x) * cpi + ci;
+  if (ci >= cpi || c0 >= C || cell >= ncells) return;
   float a[VEC][kK];
 #pragma unroll
   for (int v = 0; v < VEC; ++v) load_wvec<WDT, kK>(w, static_cast<int64_t>(c0 + v) * kK, a[v]);
 
   const Off row_b = static_cast<Off>(static_cast<int64_t>(G) * kS * C * ES);  // one high-res row, bytes
   const Off tap_b = static_cast<Off>(C * ES);
-  const int64_t row_skip = 3 * static_cast<int64_t>(G) * kS * C;
-  const int64_t cb = static_cast<int64_t>(blockIdx.x) * cpb;
-  const int64_t ce = std::min(ncells, cb + cpb);
-  CellWalk cw;
-  cw.init(cb + ci, G, C);
-  for (int64_t cell = cb + ci; cell < ce; cell += cpi) {
-    const Off xo = static_cast<Off>((cw.hoff + c0) * ES);
+  const int64_t S = static_cast<int64_t>(gridDim.x) * cpi;
+  const Off step_x = static_cast<Off>((S / G) * kS * row_b);
+  const Off step_z = static_cast<Off>(S * C * ES);
+  Off xo = static_cast<Off>((cell_hoff(cell, G, C) + c0) * ES);
+  Off zo = static_cast<Off>((cell * C + c0) * ES);
+  for (; cell < ncells; cell += S, xo += step_x, zo += step_z) {
     Raw<DT, VEC> xr[kK];
 #pragma unroll
     for (int k = 0; k < kK; ++k) load_at<DT, VEC, true>(x, xo + (k / kS) * row_b + (k % kS) * tap_b, xr[k]);
-    const Off zo = static_cast<Off>((cw.zoff + c0) * ES);
-    for (int i = 0; i < cpi; ++i) cw.next(G, C, row_skip);
     LTHC_PHASE_BARRIER();
     float acc[VEC];
 #pragma unroll
@@ -287,6 +316,84 @@ __global__ __launch_bounds__(kBlock) void read_fwd_kernel(const void* __restrict
       for (int v = 0; v < VEC; ++v) acc[v] = fmaf(xv[v], a[v][k], acc[v]);
     }
     store_at<DT, VEC>(z, zo, acc);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// WHOLE-CELL MATERIALISE / WRITE (depth <= 12, tensors below 4 GiB):
+// out[cell,k,c] = base[cell,k,c] + sum_l beta_l[c,k] dz_l[cell,c]
+// Thread = CPT channels x all 16 taps of a cell, so each dz run is loaded by
+// exactly one lane (no re-requests of the same line by several waves), and
+// its LMAX x CPT x 16 write weights stay in VGPRs.  Block = 256 threads = one
+// slab of 256*CPT channels; a wavefront access is a contiguous 64*CPT-element
+// run of one tap.  Cells are visited grid-stride with gridDim.x % G == 0 and
+// gridDim.x * gridDim.y no larger than the resident block count, so the whole
+// grid sweeps one compact window of cells at a time with no tail round.
+// When L < LMAX (EXACT == false) the padding layers load layer 0 and
+// contribute a selected 0.
+// Accumulation: acc = base, acc = fma(beta_l, dz_l, acc) for l = 0..L-1
+// (local_thc_triton_kernels.py:367-403).  Base reads and output writes are
+// streaming (non-temporal).
+// ---------------------------------------------------------------------------
+template <int DT, int WDT, int LMAX, int CPT, bool HAS_BASE, bool EXACT>
+__global__ __launch_bounds__(kBlock) void cell_mat_kernel(const void* __restrict__ base, PtrPack dz, PtrPack beta,
+                                                          void* __restrict__ out, int L, uint32_t ncells, int G,
+                                                          int C) {
+  constexpr int ES = Fmt<DT>::bytes;
+  const int c0 = (blockIdx.y * kBlock + threadIdx.x) * CPT;
+  uint32_t cell = blockIdx.x;
+  if (c0 >= C || cell >= ncells) return;
+  float bw[LMAX][CPT][kK];
+#pragma unroll
+  for (int l = 0; l < LMAX; ++l) {
+    const void* bp = beta.p[(EXACT || l < L) ? l : 0];
+#pragma unroll
+    for (int v = 0; v < CPT; ++v) load_wvec<WDT, kK>(bp, static_cast<int64_t>(c0 + v) * kK, bw[l][v]);
+  }
+  const uint32_t tap_b = C * ES;
+  const uint32_t row_b = G * kS * tap_b;
+  const uint32_t P = gridDim.x;
+  const uint32_t step_x = (P / G) * kS * row_b;
+  const uint32_t step_z = P * tap_b;
+  uint32_t xo = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES);
+  uint32_t zo = (cell * C + c0) * ES;
+  for (; cell < ncells; cell += P, xo += step_x, zo += step_z) {
+    Raw<DT, CPT> xr[kK];
+    Raw<DT, CPT> dr[LMAX];
+    if constexpr (HAS_BASE) {
+#pragma unroll
+      for (int k = 0; k < kK; ++k) load_at<DT, CPT, true>(base, xo + (k / kS) * row_b + (k % kS) * tap_b, xr[k]);
+    }
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) load_at<DT, CPT>(dz.p[(EXACT || l < L) ? l : 0], zo, dr[l]);
+    LTHC_PHASE_BARRIER();
+
+    float acc[kK][CPT];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) {
+      if constexpr (HAS_BASE) {
+        unpack_raw<DT, CPT>(xr[k], acc[k]);
+      } else {
+#pragma unroll
+        for (int v = 0; v < CPT; ++v) acc[k][v] = 0.f;
+      }
+    }
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) {
+      float d[CPT];
+      unpack_raw<DT, CPT>(dr[l], d);
+      if constexpr (!EXACT) {
+        const bool live = l < L;
+#pragma unroll
+        for (int v = 0; v < CPT; ++v) d[v] = live ? d[v] : 0.f;
+      }
+#pragma unroll
+      for (int k = 0; k < kK; ++k)
+#pragma unroll
+        for (int v = 0; v < CPT; ++v) acc[k][v] = fmaf(bw[l][v][k], d[v], acc[k][v]);
+    }
+#pragma unroll
+    for (int k = 0; k < kK; ++k) store_at<DT, CPT, true>(out, xo + (k / kS) * row_b + (k % kS) * tap_b, acc[k]);
   }
 }
 
@@ -556,16 +663,16 @@ __global__ __launch_bounds__(256) void gamma_kernel(const void* __restrict__ alp
 
 // ---------------------------------------------------------------------------
 // RECURRENCE: z_next = fma(gamma, dz, z).  Block = 64 channel quads x 4 row
-// lanes; each thread keeps its 4 gammas and walks rows with stride 4, RU
-// rows per phase (loads of rows past the end are clamped to the last row and
-// their results dropped).
+// lanes; each thread keeps its 4 gammas.  A block handles chunks of 4 * RU
+// consecutive rows, grid-stride over the chunks, RU rows per phase (loads of
+// rows past the end are clamped to the last row and their results dropped).
 // ---------------------------------------------------------------------------
 constexpr int kRU = 4;
 
 template <int DT, typename Off>
 __global__ __launch_bounds__(256) void recur_fwd_kernel(const void* __restrict__ z, const void* __restrict__ dz,
                                                         const void* __restrict__ gamma, int gdt,
-                                                        void* __restrict__ zn, int64_t rows, int C, int64_t rpb) {
+                                                        void* __restrict__ zn, int64_t rows, int C) {
   constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int c0 = (blockIdx.x * 64 + (t & 63)) * 4;
@@ -573,9 +680,10 @@ __global__ __launch_bounds__(256) void recur_fwd_kernel(const void* __restrict__
   float gm[4];
 #pragma unroll
   for (int v = 0; v < 4; ++v) gm[v] = load_w(gamma, gdt, c0 + v);
-  const int64_t rb = static_cast<int64_t>(blockIdx.y) * rpb;
-  const int64_t re = std::min(rows, rb + rpb);
-  for (int64_t r0 = rb + (t >> 6); r0 < re; r0 += 4 * kRU) {
+  // grid-stride over chunks of 4 * kRU rows: block y owns chunks y, y + gridDim.y, ...
+  const int64_t re = rows;
+  const int64_t S = static_cast<int64_t>(4 * kRU) * gridDim.y;
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.y) * 4 * kRU + (t >> 6); r0 < re; r0 += S) {
     Raw<DT, 4> ar[kRU], dr[kRU];
     Off off[kRU];
 #pragma unroll
@@ -734,9 +842,10 @@ WgradPlan wgrad_plan(int64_t ncells, int64_t C, int L, int blocks_per_cu = 2) {
   return p;
 }
 
-// Rows per block of the recurrence kernels (forward: more, smaller blocks
-// measured faster; backward: fewer partial rows to reduce).
-const int64_t kRecurRowsPerBlock = 64;
+// Recurrence forward: row chunks (of 4 * kRU rows) in flight per channel
+// block column, measured best at 1024 on MI355X.  Backward: rows per block
+// (fewer partial rows to reduce).
+const int64_t kRecurChunks = 1024;
 const int64_t kRecurBwdRowsPerBlock = 256;
 
 template <int V>
@@ -781,26 +890,36 @@ void dispatch_off(bool off32, F&& f) {
   else f(TypeTag<int64_t>{});
 }
 
-constexpr int kReadBlocksPerCU = 8;
+// Grid-stride cell sweeps need the cells covered per grid step to be a
+// multiple of G (constant offset increments) and of `cpi` (cells per block).
+// Returns the step closest below `want` cells, at least one such multiple and
+// at most ncells rounded up.
+int64_t grid_step_cells(int64_t want, int64_t ncells, int G, int cpi) {
+  const int64_t unit = std::lcm<int64_t>(G, cpi);
+  const int64_t cap = (ncells + unit - 1) / unit * unit;
+  return std::max<int64_t>(unit, std::min<int64_t>(want / unit * unit, cap));
+}
+
+// Read blocks per CU (one: measured best for the 16-tap vector loads).
+constexpr int kReadBlocksPerCU = 1;
 
 template <int DT, int WDT, typename Off>
-void launch_read(const void* x, const void* w, void* z, int64_t ncells, int G, int C, bool vec8, hipStream_t st,
-                 int blocks_per_cu = kReadBlocksPerCU) {
+void launch_read(const void* x, const void* w, void* z, int64_t ncells, int G, int C, bool vec8, hipStream_t st) {
   const int vec = vec8 ? 8 : 4;
   const int ncv = C / vec;
   const int ncv_blk = std::min(ncv, kBlock);
   const int cpi = kBlock / ncv_blk;
   const int gy = (ncv + ncv_blk - 1) / ncv_blk;
-  const int64_t cpb = std::max<int64_t>(cpi, cells_per_block(ncells, gy, blocks_per_cu));
-  const dim3 grid(static_cast<unsigned>((ncells + cpb - 1) / cpb), gy);
+  const int64_t step = grid_step_cells(static_cast<int64_t>(num_cus()) * kReadBlocksPerCU * cpi / gy, ncells, G, cpi);
+  const dim3 grid(static_cast<unsigned>(step / cpi), gy);
   const dim3 block(ncv_blk * cpi);
   if constexpr (DT != LTHC_F32) {
     if (vec8) {
-      read_fwd_kernel<DT, WDT, 8, Off><<<grid, block, 0, st>>>(x, w, z, ncells, G, C, ncv_blk, cpi, cpb);
+      read_fwd_kernel<DT, WDT, 8, Off><<<grid, block, 0, st>>>(x, w, z, ncells, G, C, ncv_blk, cpi);
       return;
     }
   }
-  read_fwd_kernel<DT, WDT, 4, Off><<<grid, block, 0, st>>>(x, w, z, ncells, G, C, ncv_blk, cpi, cpb);
+  read_fwd_kernel<DT, WDT, 4, Off><<<grid, block, 0, st>>>(x, w, z, ncells, G, C, ncv_blk, cpi);
 }
 
 // Thread shapes (taps x channels per thread) of the register-resident weight
@@ -855,15 +974,59 @@ void launch_mat_l(const void* base, const PtrPack& dz, const PtrPack& beta, void
     launch_mat_t<DT, WDT, LMAX, TPT, CPT, true, false, true, uint32_t>(base, dz, beta, out, L, ncells, G, C, kMatBlocksPerCU, st);
 }
 
+// Channels per thread of the whole-cell kernel per depth bucket: the
+// LMAX x CPT x 16 fp32 weights, one cell's loads and the 16 x CPT
+// accumulators fit in 256 VGPRs.
+template <int DT, int LMAX>
+struct CellMatShape {
+  static constexpr int CPT = DT == LTHC_F32 ? (LMAX <= 1 ? 2 : 1) : (LMAX <= 1 ? 4 : (LMAX <= 4 ? 2 : 1));
+};
+
+// Blocks of `kernel` (kBlock threads) resident on one CU.
+template <typename K>
+int resident_blocks(K kernel) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kBlock, 0) != hipSuccess || n < 1) n = 1;
+  return n;
+}
+
+template <int DT, int WDT, int LMAX, bool HAS_BASE, bool EXACT>
+void launch_cell_mat(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells, int G,
+                     int C, hipStream_t st) {
+  constexpr int CPT = CellMatShape<DT, LMAX>::CPT;
+  const auto kernel = cell_mat_kernel<DT, WDT, LMAX, CPT, HAS_BASE, EXACT>;
+  static const int per_cu = resident_blocks(kernel);
+  const int slabs = (C / CPT + kBlock - 1) / kBlock;
+  const int64_t per = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu / slabs, ncells, G, 1);
+  kernel<<<dim3(static_cast<unsigned>(per), slabs), kBlock, 0, st>>>(base, dz, beta, out, L,
+                                                                    static_cast<uint32_t>(ncells), G, C);
+}
+
+template <int DT, int WDT, int LMAX>
+void launch_cell_mat_l(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells,
+                       int G, int C, hipStream_t st) {
+  if (L == LMAX) launch_cell_mat<DT, WDT, LMAX, true, true>(base, dz, beta, out, L, ncells, G, C, st);
+  else launch_cell_mat<DT, WDT, LMAX, true, false>(base, dz, beta, out, L, ncells, G, C, st);
+}
+
 template <int DT, int WDT>
 void launch_materialise(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells,
                         int G, int C, hipStream_t st) {
   const bool off32 = fits32(ncells * kK * C * Fmt<DT>::bytes);
   if (base == nullptr) {  // the plain write: one layer, no base (validated by the caller)
-    dispatch_off(off32, [&](auto o) {
-      launch_mat_t<DT, WDT, 1, 4, 4, false, true, true, typename decltype(o)::type>(base, dz, beta, out, 1, ncells, G,
-                                                                                    C, kMatBlocksPerCU, st);
-    });
+    if (off32) {
+      launch_cell_mat<DT, WDT, 1, false, true>(base, dz, beta, out, 1, ncells, G, C, st);
+    } else {
+      launch_mat_t<DT, WDT, 1, 4, 4, false, true, true, int64_t>(base, dz, beta, out, 1, ncells, G, C, kMatBlocksPerCU, st);
+    }
+    return;
+  }
+  if (off32 && L <= 12) {  // whole-cell kernel: weights of every tap in VGPRs
+    if (L <= 1) launch_cell_mat_l<DT, WDT, 1>(base, dz, beta, out, L, ncells, G, C, st);
+    else if (L <= 2) launch_cell_mat_l<DT, WDT, 2>(base, dz, beta, out, L, ncells, G, C, st);
+    else if (L <= 4) launch_cell_mat_l<DT, WDT, 4>(base, dz, beta, out, L, ncells, G, C, st);
+    else if (L <= 8) launch_cell_mat_l<DT, WDT, 8>(base, dz, beta, out, L, ncells, G, C, st);
+    else launch_cell_mat_l<DT, WDT, 12>(base, dz, beta, out, L, ncells, G, C, st);
     return;
   }
   if (L <= 1) launch_mat_l<DT, WDT, 1>(base, dz, beta, out, L, ncells, G, C, off32, st);
@@ -1102,13 +1265,14 @@ int lthc_recur_fwd(const void* z, const void* dz, int x_dtype, const void* gamma
   if (int rc = check_act(fn, dz, x_dtype, "dz")) return rc;
   if (int rc = check_act(fn, z_next, x_dtype, "z_next")) return rc;
   if (gamma == nullptr) return fail(LTHC_ERR_INVALID, fn, "gamma is NULL");
-  const dim3 grid(static_cast<unsigned>((C / 4 + 63) / 64), static_cast<unsigned>((rows + kRecurRowsPerBlock - 1) / kRecurRowsPerBlock));
+  const int64_t chunks = (rows + 4 * kRU - 1) / (4 * kRU);
+  const dim3 grid(static_cast<unsigned>((C / 4 + 63) / 64), static_cast<unsigned>(std::min(chunks, kRecurChunks)));
   const hipStream_t st = static_cast<hipStream_t>(stream);
   const bool off32 = fits32(rows * C * esize(x_dtype));
   dispatch_dtype(x_dtype, [&](auto d) {
     dispatch_off(off32, [&](auto o) {
       recur_fwd_kernel<decltype(d)::value, typename decltype(o)::type>
-          <<<grid, 256, 0, st>>>(z, dz, gamma, g_dtype, z_next, rows, static_cast<int>(C), kRecurRowsPerBlock);
+          <<<grid, 256, 0, st>>>(z, dz, gamma, g_dtype, z_next, rows, static_cast<int>(C));
     });
   });
   return check_launch(fn);
