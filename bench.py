@@ -53,9 +53,10 @@ def parse_args():
     p.add_argument("--no-model", action="store_true", help="skip the LTHC-B/4 forward leg")
     p.add_argument(
         "--profile",
-        choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy"],
+        choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model"],
         help="run only this kernel --steps times at the configured shape (for rocprofv3), plus one plain copy "
-        "of X0 (a copy kernel of known size that calibrates the FETCH_SIZE / WRITE_SIZE counters)",
+        "of X0 (a copy kernel of known size that calibrates the FETCH_SIZE / WRITE_SIZE counters); 'model' runs "
+        "only the LTHC-B/4 forward leg",
     )
     return p.parse_args()
 
@@ -239,6 +240,9 @@ def main():
         print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
         sys.exit(1)
     dev = torch.device("cuda:0")
+    if args.profile == "model":
+        print(json.dumps({"model_fwd": model_forward(args, torch, dev)}))
+        return
     B, G, C, L = args.batch, args.grid, args.channels, args.depth
     H = 4 * G
     bf16 = torch.bfloat16
