@@ -51,6 +51,8 @@ def parse_args():
     p.add_argument("--model-batch", type=int, default=64, help="batch of the LTHC-B/4 forward leg (fwd img/s)")
     p.add_argument("--model-steps", type=int, default=10)
     p.add_argument("--no-model", action="store_true", help="skip the LTHC-B/4 forward leg")
+    p.add_argument("--train-batch", type=int, default=64, help="batch of the interface fwd+bwd leg (configuration 3)")
+    p.add_argument("--no-train", action="store_true", help="skip the interface fwd+bwd leg")
     p.add_argument(
         "--profile",
         choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model"],
@@ -198,6 +200,74 @@ def model_forward(args, torch, dev):
     }
 
 
+def interface_train(args, torch, dev, ops):
+    """the interface forward + autograd backward at the training shape (B=64, bf16).
+
+    X0, alpha, the 12 beta_l and the 12 dZ_l are leaves that require grad; the upstream gradients are
+    G_L = dL/dX_L ~ N(0, 1e-3) and H_l = dL/dZ_l ~ N(0, 1e-3) for the 12 workspace states Z_0..Z_11 that feed
+    the branches.  One step = read, gamma stack, 12 recurrence steps, 12-pointer materialise, then
+    torch.autograd.backward over (X_L, Z_0..Z_11) -- every backward kernel of the interface plus autograd's own
+    gradient accumulation (adds), as in training."""
+    B, G, C, L = args.train_batch, args.grid, args.channels, args.depth
+    H = 4 * G
+    bf16 = torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(3)
+    x0 = torch.randn((B, H, H, C), generator=gen, device=dev).to(bf16).requires_grad_()
+    alpha = (torch.randn((C, 16), generator=gen, device=dev) * 0.01 + 1.0 / 16.0).requires_grad_()
+    betas = [(torch.randn((C, 16), generator=gen, device=dev) * 0.02).requires_grad_() for _ in range(L)]
+    dzs = [(torch.randn((B, G * G, C), generator=gen, device=dev) * 0.02).to(bf16).requires_grad_() for _ in range(L)]
+    g_out = (torch.randn((B, H, H, C), generator=gen, device=dev) * 1e-3).to(bf16)
+    h_ws = [(torch.randn((B, G * G, C), generator=gen, device=dev) * 1e-3).to(bf16) for _ in range(L)]
+    stream = torch.cuda.current_stream()
+
+    def forward():
+        z = ops.local_write_traceable(x0, alpha.to(bf16))
+        gam = ops.lazy_gamma_stack(alpha.to(bf16), torch.stack([b.to(bf16) for b in betas]))
+        zs = [z]
+        for l in range(L):
+            z = ops.lazy_workspace_update(z, dzs[l], gam[l])
+            zs.append(z)
+        xl = ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas) if L == 12 else None
+        return xl, zs[:L]
+
+    def step():
+        xl, zs = forward()
+        torch.autograd.backward([xl] + zs, [g_out] + h_ws)
+        for t in [x0, alpha] + betas + dzs:
+            t.grad = None
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    e0.record(stream)
+    for _ in range(args.steps):
+        with torch.no_grad():
+            forward()
+    e1.record(stream)
+    for _ in range(args.steps):
+        step()
+    e2.record(stream)
+    torch.cuda.synchronize()
+    fwd_ms = e0.elapsed_time(e1) / args.steps
+    step_ms = e1.elapsed_time(e2) / args.steps
+    T = B * H * H * C
+    W = B * G * G * C
+    fused_bwd = 2 * (3 * T + 3 * L * W)
+    return {
+        "workload": "interface fwd + autograd bwd, configuration 3 (B=64, C=768, L=12, bf16, fp32 weights)",
+        "batch": B,
+        "steps": args.steps,
+        "fwd_ms": round(fwd_ms, 4),
+        "fwd_bwd_ms": round(step_ms, 4),
+        "bwd_ms": round(step_ms - fwd_ms, 4),
+        "bwd_single_pass_bytes": fused_bwd,
+        "bwd_single_pass_GBps": round(fused_bwd / ((step_ms - fwd_ms) * 1e-3) / 1e9, 1),
+        "byte_definition": "bwd_single_pass_bytes = e*(3T + 3LW): the compulsory bytes of a fused backward "
+        "(read G_L, X0, H stack, dZ stack; write dX0, dZ-grad stack); the ops launched move more",
+    }
+
+
 def profile(args, ops, inputs, alpha, beta_stack, betas):
     """One kernel, --warmup + --steps launches, then a plain copy of X0 (bytes known: 2 x X0)."""
     import torch
@@ -341,6 +411,7 @@ def main():
     del sets, graphs
     torch.cuda.empty_cache()
     model_fwd = None if args.no_model else model_forward(args, torch, dev)
+    train = None if args.no_train else interface_train(args, torch, dev, ops)
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -385,6 +456,7 @@ def main():
         },
         "cpu_baseline": cpu,
         "model_fwd": model_fwd,
+        "interface_train": train,
         "extra": {
             "eager_ms_per_step": round(eager_ms, 4),
             "graph_ms_per_step": None if graph_ms is None else round(graph_ms, 4),

@@ -631,6 +631,125 @@ __global__ __launch_bounds__(kBlock) void wgrad_partial_kernel(const void* __res
 
 // Zero fill by a kernel rather than hipMemsetAsync, so that callers may
 // capture these launches in a HIP graph.
+// ---------------------------------------------------------------------------
+// WHOLE-CELL MULTI-WEIGHT READ (depth <= 12, tensors below 4 GiB):
+//   out_l[cell,c] = sum_k w_l[c,k] g[cell,k,c]
+// Thread = CPT channels x all 16 taps x all LMAX layers, so each g run is
+// loaded by exactly one lane; the LMAX x CPT x 16 weights stay in VGPRs.
+// Grid and cell order as cell_mat_kernel.  Padding layers (l >= L) load
+// layer 0's weights and are never stored.
+// Accumulation order k = 0..15 (local_thc_triton_kernels.py:580-592).
+// ---------------------------------------------------------------------------
+template <int DT, int WDT, int LMAX, int CPT>
+__global__ __launch_bounds__(kBlock) void cell_read_multi_kernel(const void* __restrict__ g, PtrPack w, PtrPack out,
+                                                                 int L, uint32_t ncells, int G, int C) {
+  constexpr int ES = Fmt<DT>::bytes;
+  const int c0 = (blockIdx.y * kBlock + threadIdx.x) * CPT;
+  uint32_t cell = blockIdx.x;
+  if (c0 >= C || cell >= ncells) return;
+  float wr[LMAX][CPT][kK];
+#pragma unroll
+  for (int l = 0; l < LMAX; ++l)
+#pragma unroll
+    for (int v = 0; v < CPT; ++v) load_wvec<WDT, kK>(w.p[l < L ? l : 0], static_cast<int64_t>(c0 + v) * kK, wr[l][v]);
+  const uint32_t tap_b = C * ES;
+  const uint32_t row_b = G * kS * tap_b;
+  const uint32_t P = gridDim.x;
+  const uint32_t step_x = (P / G) * kS * row_b;
+  const uint32_t step_z = P * tap_b;
+  uint32_t go = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES);
+  uint32_t zo = (cell * C + c0) * ES;
+  for (; cell < ncells; cell += P, go += step_x, zo += step_z) {
+    Raw<DT, CPT> gr[kK];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) load_at<DT, CPT, true>(g, go + (k / kS) * row_b + (k % kS) * tap_b, gr[k]);
+    LTHC_PHASE_BARRIER();
+    float acc[LMAX][CPT];
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l)
+#pragma unroll
+      for (int v = 0; v < CPT; ++v) acc[l][v] = 0.f;
+#pragma unroll
+    for (int k = 0; k < kK; ++k) {
+      float gv[CPT];
+      unpack_raw<DT, CPT>(gr[k], gv);
+#pragma unroll
+      for (int l = 0; l < LMAX; ++l)
+#pragma unroll
+        for (int v = 0; v < CPT; ++v) acc[l][v] = fmaf(gv[v], wr[l][v][k], acc[l][v]);
+    }
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l)
+      if (l < L) store_at<DT, CPT>(const_cast<void*>(out.p[l]), zo, acc[l]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// WHOLE-CELL CELL WEIGHT GRADIENT, stage 1 (depth <= 12, tensors below 4 GiB):
+//   partial[bx, l, c, k] = sum_{cells of block column bx} high[cell,k,c] low_l[cell,c]
+// Thread = CPT channels x all 16 taps; its LMAX x CPT x 16 fp32 accumulators
+// stay in VGPRs over the block column's grid-stride cells (each low run is
+// loaded by one lane).  Every block writes its partial slot, zeros included.
+// Padding layers accumulate layer 0 and are never written.
+// ---------------------------------------------------------------------------
+template <int DT, int LMAX, int CPT>
+__global__ __launch_bounds__(kBlock) void cell_wgrad_kernel(const void* __restrict__ high, PtrPack low,
+                                                            float* __restrict__ partial, int L, uint32_t ncells, int G,
+                                                            int C) {
+  constexpr int ES = Fmt<DT>::bytes;
+  const int c0 = (blockIdx.y * kBlock + threadIdx.x) * CPT;
+  if (c0 >= C) return;
+  float acc[LMAX][CPT][kK];
+#pragma unroll
+  for (int l = 0; l < LMAX; ++l)
+#pragma unroll
+    for (int v = 0; v < CPT; ++v)
+#pragma unroll
+      for (int k = 0; k < kK; ++k) acc[l][v][k] = 0.f;
+  const uint32_t tap_b = C * ES;
+  const uint32_t row_b = G * kS * tap_b;
+  const uint32_t P = gridDim.x;
+  const uint32_t step_x = (P / G) * kS * row_b;
+  const uint32_t step_z = P * tap_b;
+  uint32_t cell = blockIdx.x;
+  uint32_t ho = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES);
+  uint32_t zo = (cell * C + c0) * ES;
+  for (; cell < ncells; cell += P, ho += step_x, zo += step_z) {
+    Raw<DT, CPT> hr[kK];
+    Raw<DT, CPT> dr[LMAX];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) load_at<DT, CPT, true>(high, ho + (k / kS) * row_b + (k % kS) * tap_b, hr[k]);
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) load_at<DT, CPT>(low.p[l < L ? l : 0], zo, dr[l]);
+    LTHC_PHASE_BARRIER();
+    float h[kK][CPT];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) unpack_raw<DT, CPT>(hr[k], h[k]);
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) {
+      float d[CPT];
+      unpack_raw<DT, CPT>(dr[l], d);
+#pragma unroll
+      for (int v = 0; v < CPT; ++v)
+#pragma unroll
+        for (int k = 0; k < kK; ++k) acc[l][v][k] = fmaf(h[k][v], d[v], acc[l][v][k]);
+    }
+  }
+  float* dst = partial + static_cast<int64_t>(blockIdx.x) * L * C * kK;
+#pragma unroll
+  for (int l = 0; l < LMAX; ++l) {
+    if (l < L) {
+#pragma unroll
+      for (int v = 0; v < CPT; ++v) {
+        float4* row = reinterpret_cast<float4*>(dst + (static_cast<int64_t>(l) * C + c0 + v) * kK);
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+          row[q] = make_float4(acc[l][v][4 * q], acc[l][v][4 * q + 1], acc[l][v][4 * q + 2], acc[l][v][4 * q + 3]);
+      }
+    }
+  }
+}
+
 __global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ out, int64_t n) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i < n) out[i] = 0.f;
@@ -817,29 +936,30 @@ int64_t cells_per_block(int64_t ncells, int64_t slabs, int blocks_per_cu) {
   return std::max<int64_t>(1, (ncells + target - 1) / target);
 }
 
-// Launch plan of the weight-gradient kernel, shared with its workspace query.
-struct WgradPlan {
-  int tpt;
-  int slabs;
-  int64_t cpb;
-  int64_t nbx;
+// Grid-stride cell sweeps need the cells covered per grid step to be a
+// multiple of G (constant offset increments) and of `cpi` (cells per block).
+// Returns the step closest below `want` cells, at least one such multiple and
+// at most ncells rounded up.
+int64_t grid_step_cells(int64_t want, int64_t ncells, int G, int cpi) {
+  const int64_t unit = std::lcm<int64_t>(G, cpi);
+  const int64_t cap = (ncells + unit - 1) / unit * unit;
+  return std::max<int64_t>(unit, std::min<int64_t>(want / unit * unit, cap));
+}
+
+// Channels per thread of the whole-cell kernels per depth bucket: the
+// LMAX x CPT x 16 fp32 weights, one cell's loads and the 16 x CPT
+// accumulators fit in 256 VGPRs.
+template <int DT, int LMAX>
+struct CellMatShape {
+  static constexpr int CPT = DT == LTHC_F32 ? (LMAX <= 1 ? 2 : 1) : (LMAX <= 1 ? 4 : (LMAX <= 4 ? 2 : 1));
 };
 
-template <int LMAX>
-struct CellShape;
-
-// (TPT, CPT) of the weight-gradient kernel for depth L (the CellShape bucket).
-void wgrad_shape(int L, int& tpt, int& cpt);
-
-WgradPlan wgrad_plan(int64_t ncells, int64_t C, int L, int blocks_per_cu = 2) {
-  WgradPlan p;
-  int cpt = 4;
-  wgrad_shape(L, p.tpt, cpt);
-  const int qs = kBlock / (kK / p.tpt);
-  p.slabs = static_cast<int>((C / cpt + qs - 1) / qs);
-  p.cpb = cells_per_block(ncells, p.slabs, blocks_per_cu);
-  p.nbx = ncells > 0 ? (ncells + p.cpb - 1) / p.cpb : 0;
-  return p;
+// Blocks of `kernel` (kBlock threads) resident on one CU.
+template <typename K>
+int resident_blocks(K kernel) {
+  int n = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kBlock, 0) != hipSuccess || n < 1) n = 1;
+  return n;
 }
 
 // Recurrence forward: row chunks (of 4 * kRU rows) in flight per channel
@@ -890,14 +1010,50 @@ void dispatch_off(bool off32, F&& f) {
   else f(TypeTag<int64_t>{});
 }
 
-// Grid-stride cell sweeps need the cells covered per grid step to be a
-// multiple of G (constant offset increments) and of `cpi` (cells per block).
-// Returns the step closest below `want` cells, at least one such multiple and
-// at most ncells rounded up.
-int64_t grid_step_cells(int64_t want, int64_t ncells, int G, int cpi) {
-  const int64_t unit = std::lcm<int64_t>(G, cpi);
-  const int64_t cap = (ncells + unit - 1) / unit * unit;
-  return std::max<int64_t>(unit, std::min<int64_t>(want / unit * unit, cap));
+// Launch plan of the weight-gradient kernels, shared with the workspace query.
+struct WgradPlan {
+  bool cell;     // whole-cell grid-stride kernel (depth <= 12, tensors below 4 GiB)
+  int tpt;       // taps per thread of the block-range kernel
+  int slabs;     // channel slabs (grid y)
+  int64_t cpb;   // cells per block of the block-range kernel
+  int64_t nbx;   // blocks per slab = partial slots
+};
+
+template <int LMAX>
+struct CellShape;
+
+// (TPT, CPT) of the block-range weight-gradient kernel for depth L (the CellShape bucket).
+void wgrad_shape(int L, int& tpt, int& cpt);
+
+template <int DT, int LMAX>
+void cell_wgrad_plan_l(WgradPlan& p, int64_t ncells, int G, int64_t C) {
+  constexpr int CPT = CellMatShape<DT, LMAX>::CPT;
+  static const int per_cu = resident_blocks(cell_wgrad_kernel<DT, LMAX, CPT>);
+  p.slabs = static_cast<int>((C / CPT + kBlock - 1) / kBlock);
+  p.nbx = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu / p.slabs, ncells, G, 1);
+}
+
+WgradPlan wgrad_plan(int dt, int64_t ncells, int G, int64_t C, int L, int blocks_per_cu = 2) {
+  WgradPlan p{};
+  if (ncells > 0 && L <= 12 && fits32(ncells * kK * C * esize(dt))) {
+    p.cell = true;
+    dispatch_dtype(dt, [&](auto d) {
+      constexpr int DT = decltype(d)::value;
+      if (L <= 1) cell_wgrad_plan_l<DT, 1>(p, ncells, G, C);
+      else if (L <= 2) cell_wgrad_plan_l<DT, 2>(p, ncells, G, C);
+      else if (L <= 4) cell_wgrad_plan_l<DT, 4>(p, ncells, G, C);
+      else if (L <= 8) cell_wgrad_plan_l<DT, 8>(p, ncells, G, C);
+      else cell_wgrad_plan_l<DT, 12>(p, ncells, G, C);
+    });
+    return p;
+  }
+  int cpt = 4;
+  wgrad_shape(L, p.tpt, cpt);
+  const int qs = kBlock / (kK / p.tpt);
+  p.slabs = static_cast<int>((C / cpt + qs - 1) / qs);
+  p.cpb = cells_per_block(ncells, p.slabs, blocks_per_cu);
+  p.nbx = ncells > 0 ? (ncells + p.cpb - 1) / p.cpb : 0;
+  return p;
 }
 
 // Read blocks per CU (one: measured best for the 16-tap vector loads).
@@ -974,22 +1130,6 @@ void launch_mat_l(const void* base, const PtrPack& dz, const PtrPack& beta, void
     launch_mat_t<DT, WDT, LMAX, TPT, CPT, true, false, true, uint32_t>(base, dz, beta, out, L, ncells, G, C, kMatBlocksPerCU, st);
 }
 
-// Channels per thread of the whole-cell kernel per depth bucket: the
-// LMAX x CPT x 16 fp32 weights, one cell's loads and the 16 x CPT
-// accumulators fit in 256 VGPRs.
-template <int DT, int LMAX>
-struct CellMatShape {
-  static constexpr int CPT = DT == LTHC_F32 ? (LMAX <= 1 ? 2 : 1) : (LMAX <= 1 ? 4 : (LMAX <= 4 ? 2 : 1));
-};
-
-// Blocks of `kernel` (kBlock threads) resident on one CU.
-template <typename K>
-int resident_blocks(K kernel) {
-  int n = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kernel, kBlock, 0) != hipSuccess || n < 1) n = 1;
-  return n;
-}
-
 template <int DT, int WDT, int LMAX, bool HAS_BASE, bool EXACT>
 void launch_cell_mat(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells, int G,
                      int C, hipStream_t st) {
@@ -1047,9 +1187,27 @@ void launch_wgrad_t(const void* high, const PtrPack& low, float* partial, int L,
   wgrad_partial_kernel<DT, LMAX, TPT, CPT, NT, Off><<<grid, kBlock, 0, st>>>(high, low, partial, L, ncells, G, C, p.cpb);
 }
 
+template <int DT, int LMAX>
+void launch_cell_wgrad(const void* high, const PtrPack& low, float* partial, int L, int64_t ncells, int G, int C,
+                       const WgradPlan& p, hipStream_t st) {
+  constexpr int CPT = CellMatShape<DT, LMAX>::CPT;
+  cell_wgrad_kernel<DT, LMAX, CPT><<<dim3(static_cast<unsigned>(p.nbx), p.slabs), kBlock, 0, st>>>(
+      high, low, partial, L, static_cast<uint32_t>(ncells), G, C);
+}
+
 template <int DT, typename Off>
 void launch_wgrad(const void* high, const PtrPack& low, float* partial, int L, int64_t ncells, int G, int C,
                   const WgradPlan& p, hipStream_t st) {
+  if constexpr (std::is_same_v<Off, uint32_t>) {
+    if (p.cell) {
+      if (L <= 1) launch_cell_wgrad<DT, 1>(high, low, partial, L, ncells, G, C, p, st);
+      else if (L <= 2) launch_cell_wgrad<DT, 2>(high, low, partial, L, ncells, G, C, p, st);
+      else if (L <= 4) launch_cell_wgrad<DT, 4>(high, low, partial, L, ncells, G, C, p, st);
+      else if (L <= 8) launch_cell_wgrad<DT, 8>(high, low, partial, L, ncells, G, C, p, st);
+      else launch_cell_wgrad<DT, 12>(high, low, partial, L, ncells, G, C, p, st);
+      return;
+    }
+  }
 #define LTHC_WG(LM) \
   launch_wgrad_t<DT, LM, CellShape<LM>::TPT, CellShape<LM>::CPT, true, Off>(high, low, partial, L, ncells, G, C, p, st)
   if (L <= 1) LTHC_WG(1);
@@ -1075,9 +1233,30 @@ void launch_read_multi_t(const void* g, const PtrPack& w, const PtrPack& out, in
   read_multi_kernel<DT, WDT, LC, Off><<<grid, qs * nlg, 0, st>>>(g, w, out, L, qs, ncells, G, C, cpb);
 }
 
+template <int DT, int WDT, int LMAX>
+void launch_cell_read_multi(const void* g, const PtrPack& w, const PtrPack& out, int L, int64_t ncells, int G, int C,
+                            hipStream_t st) {
+  constexpr int CPT = CellMatShape<DT, LMAX>::CPT;
+  const auto kernel = cell_read_multi_kernel<DT, WDT, LMAX, CPT>;
+  static const int per_cu = resident_blocks(kernel);
+  const int slabs = (C / CPT + kBlock - 1) / kBlock;
+  const int64_t per = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu / slabs, ncells, G, 1);
+  kernel<<<dim3(static_cast<unsigned>(per), slabs), kBlock, 0, st>>>(g, w, out, L, static_cast<uint32_t>(ncells), G, C);
+}
+
 template <int DT, int WDT, typename Off>
 void launch_read_multi(const void* g, const PtrPack& w, const PtrPack& out, int L, int64_t ncells, int G, int C,
                        hipStream_t st) {
+  if constexpr (std::is_same_v<Off, uint32_t>) {  // whole-cell kernel: every layer's weights in VGPRs
+    if (L <= 12) {
+      if (L <= 1) launch_cell_read_multi<DT, WDT, 1>(g, w, out, L, ncells, G, C, st);
+      else if (L <= 2) launch_cell_read_multi<DT, WDT, 2>(g, w, out, L, ncells, G, C, st);
+      else if (L <= 4) launch_cell_read_multi<DT, WDT, 4>(g, w, out, L, ncells, G, C, st);
+      else if (L <= 8) launch_cell_read_multi<DT, WDT, 8>(g, w, out, L, ncells, G, C, st);
+      else launch_cell_read_multi<DT, WDT, 12>(g, w, out, L, ncells, G, C, st);
+      return;
+    }
+  }
   // Two layers per thread keep 128 weights + loads + accumulators within 256
   // VGPRs; three per thread only where 16 groups of two are not enough.
   if (L == 1) launch_read_multi_t<DT, WDT, 1, Off>(g, w, out, L, ncells, G, C, st);
@@ -1193,9 +1372,12 @@ int lthc_materialise_fwd(const void* base, const void* const* dz, int x_dtype, c
 }
 
 size_t lthc_weight_grad_workspace_bytes(int64_t B, int64_t G, int64_t s, int64_t C, int L) {
-  if (B <= 0 || G <= 0 || C <= 0 || L < 1 || s != kS) return 0;
-  const WgradPlan p = wgrad_plan(B * G * G, C, L);
-  return static_cast<size_t>(p.nbx) * static_cast<size_t>(L) * static_cast<size_t>(C) * kK * sizeof(float);
+  if (B <= 0 || G <= 0 || C <= 0 || L < 1 || s != kS || C % 4 != 0 || G > 4096 || C > (1 << 24)) return 0;
+  if (B > (int64_t(1) << 40) / (G * G * kK * C)) return 0;
+  // the plan depends on the activation dtype: return the largest over the dtypes
+  int64_t nbx = 0;
+  for (int dt : {LTHC_F32, LTHC_BF16, LTHC_F16}) nbx = std::max(nbx, wgrad_plan(dt, B * G * G, static_cast<int>(G), C, L).nbx);
+  return static_cast<size_t>(nbx) * static_cast<size_t>(L) * static_cast<size_t>(C) * kK * sizeof(float);
 }
 
 int lthc_weight_grad(const void* high, const void* const* low, int x_dtype, float* gw, int64_t B, int64_t G, int64_t s,
@@ -1216,7 +1398,7 @@ int lthc_weight_grad(const void* high, const void* const* low, int x_dtype, floa
   PtrPack lp;
   if (int rc = fill_ptrs(fn, lp, low, L, "low", x_dtype, true)) return rc;
   const int64_t ncells = B * G * G;
-  const WgradPlan p = wgrad_plan(ncells, C, L);
+  const WgradPlan p = wgrad_plan(x_dtype, ncells, static_cast<int>(G), C, L);
   const size_t need = static_cast<size_t>(p.nbx) * n * sizeof(float);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(LTHC_ERR_INVALID, fn, "workspace smaller than lthc_weight_grad_workspace_bytes()");
