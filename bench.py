@@ -55,10 +55,10 @@ def parse_args():
     p.add_argument("--no-train", action="store_true", help="skip the interface fwd+bwd leg")
     p.add_argument(
         "--profile",
-        choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model"],
+        choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model", "train"],
         help="run only this kernel --steps times at the configured shape (for rocprofv3), plus one plain copy "
         "of X0 (a copy kernel of known size that calibrates the FETCH_SIZE / WRITE_SIZE counters); 'model' runs "
-        "only the LTHC-B/4 forward leg",
+        "only the LTHC-B/4 forward leg, 'train' only the interface fwd+bwd leg",
     )
     return p.parse_args()
 
@@ -142,6 +142,7 @@ def eager_interface(model, torch):
         return cells.reshape(dz.shape[0], g, g, 4, 4, c).permute(0, 1, 3, 2, 4, 5).reshape(dz.shape[0], 4 * g, 4 * g, c)
 
     model.shared_read.read = read
+    model.shared_read.read_with_residual = lambda x: (x, read(x))
     for blk in model.blocks:
         blk.lazy_workspace_update = lambda z, dz, sr, b=blk: z + b.write.gamma_from_alpha(sr.alpha(dtype=dz.dtype))[None, None, :] * dz
 
@@ -205,9 +206,9 @@ def interface_train(args, torch, dev, ops):
 
     X0, alpha, the 12 beta_l and the 12 dZ_l are leaves that require grad; the upstream gradients are
     G_L = dL/dX_L ~ N(0, 1e-3) and H_l = dL/dZ_l ~ N(0, 1e-3) for the 12 workspace states Z_0..Z_11 that feed
-    the branches.  One step = read, gamma stack, 12 recurrence steps, 12-pointer materialise, then
-    torch.autograd.backward over (X_L, Z_0..Z_11) -- every backward kernel of the interface plus autograd's own
-    gradient accumulation (adds), as in training."""
+    the branches.  One step = read (the fused-open form of the model's forward_lazy), gamma stack, 12
+    recurrence steps, 12-pointer materialise, then torch.autograd.grad over (X_L, Z_0..Z_11) -- every backward
+    kernel of the interface plus autograd's own gradient accumulation (adds), as in training."""
     B, G, C, L = args.train_batch, args.grid, args.channels, args.depth
     H = 4 * G
     bf16 = torch.bfloat16
@@ -221,48 +222,86 @@ def interface_train(args, torch, dev, ops):
     stream = torch.cuda.current_stream()
 
     def forward():
-        z = ops.local_write_traceable(x0, alpha.to(bf16))
+        x0v, z = ops.read_with_residual(x0, alpha.to(bf16))  # as the model's forward_lazy
         gam = ops.lazy_gamma_stack(alpha.to(bf16), torch.stack([b.to(bf16) for b in betas]))
         zs = [z]
         for l in range(L):
             z = ops.lazy_workspace_update(z, dzs[l], gam[l])
             zs.append(z)
-        xl = ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas) if L == 12 else None
+        xl = ops.final_accumulate_b4_12_traceable(x0v, *dzs, *betas) if L == 12 else None
         return xl, zs[:L]
+
+    leaves = [x0, alpha] + betas + dzs
 
     def step():
         xl, zs = forward()
-        torch.autograd.backward([xl] + zs, [g_out] + h_ws)
-        for t in [x0, alpha] + betas + dzs:
-            t.grad = None
+        return torch.autograd.grad([xl] + zs, leaves, [g_out] + h_ws)
+
+    def fwd_only():
+        with torch.no_grad():
+            return forward()
+
+    def timed(fn):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(args.steps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-    e0.record(stream)
-    for _ in range(args.steps):
-        with torch.no_grad():
-            forward()
-    e1.record(stream)
-    for _ in range(args.steps):
-        step()
-    e2.record(stream)
-    torch.cuda.synchronize()
-    fwd_ms = e0.elapsed_time(e1) / args.steps
-    step_ms = e1.elapsed_time(e2) / args.steps
+    eager_fwd = timed(fwd_only)
+    eager_step = timed(step)
+
+    # HIP graphs of the forward alone and of forward + backward, replayed
+    graph_fwd = graph_step = None
+    graph_error = None
+    try:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                step()
+                fwd_only()
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        g_fwd, g_step = torch.cuda.CUDAGraph(), torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g_fwd):
+            fwd_only()
+        with torch.cuda.graph(g_step):
+            grads_graph = step()
+        grads_eager = step()
+        g_step.replay()
+        torch.cuda.synchronize()
+        if not all(torch.equal(a, b) for a, b in zip(grads_graph, grads_eager)):
+            raise RuntimeError("graph replay of the training step differs from the eager step")
+        graph_fwd = timed(g_fwd.replay)
+        graph_step = timed(g_step.replay)
+    except RuntimeError as exc:  # report the eager timing with the reason
+        graph_error = str(exc)[:300]
+        torch.cuda.synchronize()
     T = B * H * H * C
     W = B * G * G * C
     fused_bwd = 2 * (3 * T + 3 * L * W)
+    fwd_ms, step_ms = (graph_fwd, graph_step) if graph_error is None else (eager_fwd, eager_step)
+    bwd_ms = step_ms - fwd_ms
     return {
         "workload": "interface fwd + autograd bwd, configuration 3 (B=64, C=768, L=12, bf16, fp32 weights)",
         "batch": B,
         "steps": args.steps,
+        "timing": "HIP graph replays (forward alone; forward + autograd.grad), eager for comparison"
+        if graph_error is None
+        else f"eager (graph capture failed: {graph_error})",
         "fwd_ms": round(fwd_ms, 4),
         "fwd_bwd_ms": round(step_ms, 4),
-        "bwd_ms": round(step_ms - fwd_ms, 4),
+        "bwd_ms": round(bwd_ms, 4),
+        "eager_fwd_ms": round(eager_fwd, 4),
+        "eager_fwd_bwd_ms": round(eager_step, 4),
         "bwd_single_pass_bytes": fused_bwd,
-        "bwd_single_pass_GBps": round(fused_bwd / ((step_ms - fwd_ms) * 1e-3) / 1e9, 1),
+        "bwd_single_pass_GBps": round(fused_bwd / (bwd_ms * 1e-3) / 1e9, 1),
         "byte_definition": "bwd_single_pass_bytes = e*(3T + 3LW): the compulsory bytes of a fused backward "
         "(read G_L, X0, H stack, dZ stack; write dX0, dZ-grad stack); the ops launched move more",
     }
@@ -312,6 +351,9 @@ def main():
     dev = torch.device("cuda:0")
     if args.profile == "model":
         print(json.dumps({"model_fwd": model_forward(args, torch, dev)}))
+        return
+    if args.profile == "train":
+        print(json.dumps({"interface_train": interface_train(args, torch, dev, ops)}))
         return
     B, G, C, L = args.batch, args.grid, args.channels, args.depth
     H = 4 * G

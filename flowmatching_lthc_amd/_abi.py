@@ -106,7 +106,13 @@ def ptr_array(ts: Sequence[torch.Tensor]):
     return (ctypes.c_void_p * len(ts))(*[t.data_ptr() for t in ts])
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
+    """The raw hipStream_t of torch's current stream on t's device."""
+    if _raw_stream is not None:
+        return _raw_stream(t.device.index)
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

@@ -765,6 +765,40 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
   out[i] = s;
 }
 
+// Narrow outputs (few columns, many partial rows): block = 16 columns x 16
+// part groups; group g sums parts g, g + 16, g + 32, ... in order, then the
+// 16 group sums are added in order g = 0..15 -- a fixed order, so the result
+// is bitwise reproducible, with 16x the parallelism of reduce_partials_kernel.
+constexpr int kRedGroups = 16;
+__global__ __launch_bounds__(256) void reduce_partials_split_kernel(const float* __restrict__ partial, int nparts,
+                                                                    int64_t n, float* __restrict__ out) {
+  __shared__ float part[kRedGroups][16];
+  const int col = threadIdx.x & 15;
+  const int grp = threadIdx.x >> 4;
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 16 + col;
+  float s = 0.f;
+  if (i < n) {
+    // loads in batches of 8 (in flight together), added in part order
+    int p = grp;
+    for (; p + 7 * kRedGroups < nparts; p += 8 * kRedGroups) {
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = partial[static_cast<int64_t>(p + j * kRedGroups) * n + i];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) s += v[j];
+    }
+    for (; p < nparts; p += kRedGroups) s += partial[static_cast<int64_t>(p) * n + i];
+  }
+  part[grp][col] = s;
+  __syncthreads();
+  if (grp == 0 && i < n) {
+    float t = 0.f;
+#pragma unroll
+    for (int g = 0; g < kRedGroups; ++g) t += part[g][col];
+    out[i] = t;
+  }
+}
+
 // ---------------------------------------------------------------------------
 // GAMMA: gamma[l, c] = sum_k alpha[c,k] beta_l[c,k], k = 0..K-1 in order
 // ---------------------------------------------------------------------------
@@ -826,11 +860,12 @@ __global__ __launch_bounds__(256) void recur_fwd_kernel(const void* __restrict__
 }
 
 // RECURRENCE BACKWARD: gdz = gamma * g; partial[4*by + lane_row, c] = sum g*dz
+// over the rows the thread visits.  Grid and row order as recur_fwd_kernel.
 template <int DT, typename Off>
 __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__ g, const void* __restrict__ dz,
                                                         const void* __restrict__ gamma, int gdt,
                                                         void* __restrict__ gdz, float* __restrict__ partial,
-                                                        int64_t rows, int C, int64_t rpb) {
+                                                        int64_t rows, int C) {
   constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int c0 = (blockIdx.x * 64 + (t & 63)) * 4;
@@ -839,9 +874,9 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
 #pragma unroll
   for (int v = 0; v < 4; ++v) gm[v] = load_w(gamma, gdt, c0 + v);
   float s[4] = {0.f, 0.f, 0.f, 0.f};
-  const int64_t rb = static_cast<int64_t>(blockIdx.y) * rpb;
-  const int64_t re = std::min(rows, rb + rpb);
-  for (int64_t r0 = rb + (t >> 6); r0 < re; r0 += 4 * kRU) {
+  const int64_t re = rows;
+  const int64_t S = static_cast<int64_t>(4 * kRU) * gridDim.y;
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.y) * 4 * kRU + (t >> 6); r0 < re; r0 += S) {
     Raw<DT, 4> ar[kRU], dr[kRU];
     Off off[kRU];
 #pragma unroll
@@ -963,10 +998,21 @@ int resident_blocks(K kernel) {
 }
 
 // Recurrence forward: row chunks (of 4 * kRU rows) in flight per channel
-// block column, measured best at 1024 on MI355X.  Backward: rows per block
-// (fewer partial rows to reduce).
+// block column, measured best at 1024 on MI355X.  Backward: 256 (each block
+// row leaves 4 partial rows of C floats to reduce).
 const int64_t kRecurChunks = 1024;
-const int64_t kRecurBwdRowsPerBlock = 256;
+const int64_t kRecurBwdChunks = 256;
+
+int64_t recur_bwd_blocks_y(int64_t rows) { return std::min((rows + 4 * kRU - 1) / (4 * kRU), kRecurBwdChunks); }
+
+// Deterministic reduction of nparts partial rows of n floats into out.
+void launch_reduce(const float* partial, int nparts, int64_t n, float* out, hipStream_t st) {
+  if (nparts <= kRedGroups) {
+    reduce_partials_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(partial, nparts, n, out);
+  } else {
+    reduce_partials_split_kernel<<<static_cast<unsigned>((n + 15) / 16), 256, 0, st>>>(partial, nparts, n, out);
+  }
+}
 
 template <int V>
 using IC = std::integral_constant<int, V>;
@@ -1412,7 +1458,7 @@ int lthc_weight_grad(const void* high, const void* const* low, int x_dtype, floa
     });
   });
   if (int rc = check_launch(fn)) return rc;
-  reduce_partials_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(partial, static_cast<int>(p.nbx), n, gw);
+  launch_reduce(partial, static_cast<int>(p.nbx), n, gw, st);
   return check_launch(fn);
 }
 
@@ -1462,8 +1508,7 @@ int lthc_recur_fwd(const void* z, const void* dz, int x_dtype, const void* gamma
 
 size_t lthc_recur_bwd_workspace_bytes(int64_t rows, int64_t C) {
   if (rows <= 0 || C <= 0) return 0;
-  const int64_t by = (rows + kRecurBwdRowsPerBlock - 1) / kRecurBwdRowsPerBlock;
-  return static_cast<size_t>(by * 4 * C) * sizeof(float);
+  return static_cast<size_t>(recur_bwd_blocks_y(rows) * 4 * C) * sizeof(float);
 }
 
 int lthc_recur_bwd(const void* g, const void* dz, int x_dtype, const void* gamma, int g_dtype, void* gdz, float* ggamma,
@@ -1485,18 +1530,18 @@ int lthc_recur_bwd(const void* g, const void* dz, int x_dtype, const void* gamma
   if (workspace == nullptr || workspace_bytes < need)
     return fail(LTHC_ERR_INVALID, fn, "workspace smaller than lthc_recur_bwd_workspace_bytes()");
   if (!aligned(workspace, 16)) return fail(LTHC_ERR_INVALID, fn, "workspace is not 16-byte aligned");
-  const int64_t by = (rows + kRecurBwdRowsPerBlock - 1) / kRecurBwdRowsPerBlock;
+  const int64_t by = recur_bwd_blocks_y(rows);
   const dim3 grid(static_cast<unsigned>((C / 4 + 63) / 64), static_cast<unsigned>(by));
   float* partial = static_cast<float*>(workspace);
   const bool off32 = fits32(rows * C * esize(x_dtype));
   dispatch_dtype(x_dtype, [&](auto d) {
     dispatch_off(off32, [&](auto o) {
       recur_bwd_kernel<decltype(d)::value, typename decltype(o)::type>
-          <<<grid, 256, 0, st>>>(g, dz, gamma, g_dtype, gdz, partial, rows, static_cast<int>(C), kRecurBwdRowsPerBlock);
+          <<<grid, 256, 0, st>>>(g, dz, gamma, g_dtype, gdz, partial, rows, static_cast<int>(C));
     });
   });
   if (int rc = check_launch(fn)) return rc;
-  reduce_partials_kernel<<<static_cast<unsigned>((C + 255) / 256), 256, 0, st>>>(partial, static_cast<int>(by * 4), C, ggamma);
+  launch_reduce(partial, static_cast<int>(by * 4), C, ggamma, st);
   return check_launch(fn);
 }
 

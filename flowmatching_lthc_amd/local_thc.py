@@ -72,6 +72,16 @@ class SharedLocalRead(nn.Module):
         alpha = _per_channel(self.alpha(dtype=x.dtype), self.group_dim)
         return ops.local_write_traceable(x, alpha)
 
+    def read_with_residual(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """(x, read(x)) for the lazy forward, where x is read once here and materialised into at the end;
+        the backward returns dX = g_x + R^T(gZ0) in one pass (ops.read_with_residual)."""
+        b, h, w, c = x.shape
+        hh = self.high_grid
+        if h != hh or w != hh or c != self.hidden_size:
+            raise ValueError(f"expected [B,{hh},{hh},{self.hidden_size}], got {tuple(x.shape)}")
+        alpha = _per_channel(self.alpha(dtype=x.dtype), self.group_dim)
+        return ops.read_with_residual(x, alpha)
+
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return self.read(x)
 

@@ -427,8 +427,7 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
 
     def forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         t6, t2 = self._conditioning(t, y)
-        x0 = self.x_embedder(x)
-        z = self.shared_read.read(x0)
+        x0, z = self.shared_read.read_with_residual(self.x_embedder(x))
         dz_list = []
         for block in self.blocks:
             dz = block.branch_update(z, t6, self.workspace_rope)

@@ -94,6 +94,24 @@ def _check_weight(w: Tensor, c: int, name: str) -> None:
     _abi.code(w)
 
 
+class _NoContext:
+    def __enter__(self):
+        return None
+
+    def __exit__(self, *exc):
+        return False
+
+
+_NO_CONTEXT = _NoContext()
+
+
+def _on_device(t: Tensor):
+    """Make t's device current for the launch (a no-op context when it already is)."""
+    if t.device.index == torch.cuda.current_device():
+        return _NO_CONTEXT
+    return torch.cuda.device(t.device)
+
+
 def _same_dtype(ref: Tensor, others: Sequence[Tensor]) -> list[Tensor]:
     return [t if t.dtype == ref.dtype else t.to(ref.dtype) for t in others]
 
@@ -102,7 +120,7 @@ def _same_dtype(ref: Tensor, others: Sequence[Tensor]) -> list[Tensor]:
 # launches (inputs already checked and prepared)
 # ---------------------------------------------------------------------------
 def _launch_read(x: Tensor, w: Tensor, z: Tensor, b: int, g: int, c: int) -> None:
-    with torch.cuda.device(x.device):
+    with _on_device(x):
         rc = _abi.load().lthc_read_fwd(
             x.data_ptr(), _abi.code(x), w.data_ptr(), _abi.code(w), z.data_ptr(), b, g, S, c, _abi.stream_of(x)
         )
@@ -112,7 +130,7 @@ def _launch_read(x: Tensor, w: Tensor, z: Tensor, b: int, g: int, c: int) -> Non
 def _launch_materialise(base: Tensor | None, dzs: Sequence[Tensor], betas: Sequence[Tensor], out: Tensor) -> None:
     b, g, c = _lo_geom(dzs[0], "dz")
     wd = _abi.code(betas[0])
-    with torch.cuda.device(out.device):
+    with _on_device(out):
         rc = _abi.load().lthc_materialise_fwd(
             _abi.ptr(base), _abi.ptr_array(dzs), _abi.code(out), _abi.ptr_array(betas), wd, out.data_ptr(),
             b, g, S, c, len(dzs), _abi.stream_of(out),
@@ -122,7 +140,7 @@ def _launch_materialise(base: Tensor | None, dzs: Sequence[Tensor], betas: Seque
 
 def _launch_read_multi(gr: Tensor, ws: Sequence[Tensor], outs: Sequence[Tensor]) -> None:
     b, g, c = _hi_geom(gr, "grad_out")
-    with torch.cuda.device(gr.device):
+    with _on_device(gr):
         rc = _abi.load().lthc_read_multi_fwd(
             gr.data_ptr(), _abi.code(gr), _abi.ptr_array(ws), _abi.code(ws[0]), _abi.ptr_array(outs),
             b, g, S, c, len(ws), _abi.stream_of(gr),
@@ -136,7 +154,7 @@ def _launch_weight_grad(high: Tensor, lows: Sequence[Tensor]) -> Tensor:
     out = torch.empty((L, c, K), device=high.device, dtype=torch.float32)
     nbytes = _abi.weight_grad_workspace_bytes(b, g, S, c, L)
     ws = torch.empty((max(nbytes, 16),), device=high.device, dtype=torch.uint8)
-    with torch.cuda.device(high.device):
+    with _on_device(high):
         rc = _abi.load().lthc_weight_grad(
             high.data_ptr(), _abi.ptr_array(lows), _abi.code(high), out.data_ptr(), b, g, S, c, L,
             ws.data_ptr(), ws.numel(), _abi.stream_of(high),
@@ -239,6 +257,89 @@ def _backward_read(ctx, grad_x):
 
 torch.library.register_autograd(local_write_traceable, _backward_write, setup_context=_setup_write_ctx)
 torch.library.register_autograd(local_read_traceable, _backward_read, setup_context=_setup_read_ctx)
+
+
+# ---------------------------------------------------------------------------
+# WRITE-ADD  (jit_thc::local_read_add_traceable, local_thc_triton_kernels.py:2713-2723)
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("jit_thc::local_read_add_traceable", mutates_args=())
+def local_read_add_traceable(z: Tensor, weight: Tensor, x: Tensor) -> Tensor:
+    """x[b,m,k,c] + weight[c,k] z[b,m,c] in x.dtype, one pass over x (the materialisation with L = 1)."""
+    _on_gpu(z, weight, x)
+    b, g, c = _lo_geom(z)
+    bx, gx, cx = _hi_geom(x)
+    if (bx, gx, cx) != (b, g, c):
+        raise ValueError(f"z {tuple(z.shape)} and x {tuple(x.shape)} do not describe the same cells")
+    _check_weight(weight, c, "weight")
+    x = _prep(x)
+    (z,) = _same_dtype(x, [_prep(z)])
+    w = _prep_w(weight, x.dtype)
+    out = torch.empty_like(x)
+    _launch_materialise(x, [z], [w], out)
+    return out
+
+
+@local_read_add_traceable.register_fake
+def _(z: Tensor, weight: Tensor, x: Tensor) -> Tensor:
+    return torch.empty_like(x)
+
+
+def _setup_read_add_ctx(ctx, inputs, output):
+    z, weight, _ = inputs
+    ctx.save_for_backward(z, weight)
+
+
+def _backward_read_add(ctx, grad_out):
+    # local_thc_triton_kernels.py:2749-2754
+    z, weight = ctx.saved_tensors
+    grad_z = local_write_traceable(grad_out, weight) if ctx.needs_input_grad[0] else None
+    grad_w = local_weight_grad_traceable(grad_out, z).to(dtype=weight.dtype) if ctx.needs_input_grad[1] else None
+    return grad_z, grad_w, grad_out
+
+
+torch.library.register_autograd(local_read_add_traceable, _backward_read_add, setup_context=_setup_read_add_ctx)
+
+
+class _OpenInterface(torch.autograd.Function):
+    """(x, Z0 = R(x)) as one autograd node.
+
+    In the lazy forward x feeds both the read and the final materialisation,
+    so autograd would write R^T(gZ0) as a full high-res tensor and then add
+    the materialisation's gradient to it (two more passes over x's size).
+    Here the node receives both gradients together and returns
+    dX = g_x + R^T(gZ0) from one local_read_add pass; dW = sum x * gZ0.
+    """
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor):
+        z = local_write_traceable(x, weight)
+        ctx.save_for_backward(x, weight)
+        return x.view_as(x), z
+
+    @staticmethod
+    def backward(ctx, grad_x: Tensor | None, grad_z: Tensor | None):
+        x, weight = ctx.saved_tensors
+        gx = gw = None
+        if grad_z is None:
+            gx = grad_x
+        else:
+            if ctx.needs_input_grad[0]:
+                if grad_x is None:
+                    gx = local_read_traceable(grad_z, weight)
+                else:
+                    gx = local_read_add_traceable(grad_z, weight, grad_x.to(x.dtype))
+            if ctx.needs_input_grad[1]:
+                gw = local_weight_grad_traceable(x, grad_z).to(dtype=weight.dtype)
+        return gx, gw
+
+
+def read_with_residual(x: Tensor, weight: Tensor) -> tuple[Tensor, Tensor]:
+    """(x, local_write_traceable(x, weight)) with a fused backward for a later consumer of x.
+
+    Values are those of the two separate uses; the backward of x is
+    g_x + R^T(gZ) in one pass instead of autograd's separate write and add.
+    """
+    return _OpenInterface.apply(x, weight)
 
 
 # ---------------------------------------------------------------------------
@@ -470,7 +571,7 @@ def lazy_workspace_update(z: Tensor, dz: Tensor, gamma: Tensor) -> Tensor:
     dt = torch.promote_types(z.dtype, dz.dtype)
     z, dz, gamma = _prep(z.to(dt)), _prep(dz.to(dt)), _prep(gamma)
     out = torch.empty_like(z)
-    with torch.cuda.device(z.device):
+    with _on_device(z):
         rc = _abi.load().lthc_recur_fwd(
             z.data_ptr(), dz.data_ptr(), _abi.code(z), gamma.data_ptr(), _abi.code(gamma), out.data_ptr(),
             z.numel() // c, c, _abi.stream_of(z),
@@ -496,7 +597,7 @@ def lazy_workspace_update_backward(grad: Tensor, dz: Tensor, gamma: Tensor) -> t
     gdz = torch.empty_like(grad)
     ggamma = torch.empty((c,), device=grad.device, dtype=torch.float32)
     ws = torch.empty((max(_abi.recur_bwd_workspace_bytes(rows, c), 16),), device=grad.device, dtype=torch.uint8)
-    with torch.cuda.device(grad.device):
+    with _on_device(grad):
         rc = _abi.load().lthc_recur_bwd(
             grad.data_ptr(), dz.data_ptr(), _abi.code(grad), gamma.data_ptr(), _abi.code(gamma), gdz.data_ptr(),
             ggamma.data_ptr(), rows, c, ws.data_ptr(), ws.numel(), _abi.stream_of(grad),
@@ -547,7 +648,7 @@ def lazy_gamma_stack(alpha: Tensor, beta_stack: Tensor) -> Tensor:
     alpha, beta_stack = alpha.contiguous(), beta_stack.contiguous()
     c, k = alpha.shape
     out = torch.empty((L, c), device=alpha.device, dtype=torch.float32)
-    with torch.cuda.device(alpha.device):
+    with _on_device(alpha):
         rc = _abi.load().lthc_gamma(
             alpha.data_ptr(), _abi.ptr_array(list(beta_stack.unbind(0))), _abi.code(alpha), out.data_ptr(),
             _abi.F32, c, k, L, _abi.stream_of(alpha),

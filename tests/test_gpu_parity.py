@@ -144,14 +144,21 @@ def test_config3_read_backward_bf16(coracle):
     assert_f32(host(da), coracle.Cweight_grad(host(x0), [host(gz)], G)[0], tol=1e-5, what="dalpha")
 
 
-def test_interface_autograd_matches_closed_form_fp32(coracle):
-    """Read op -> 4 recurrence ops -> stacked materialise op, backward through torch autograd."""
+@pytest.mark.parametrize("fused_open", [False, True])
+def test_interface_autograd_matches_closed_form_fp32(coracle, fused_open):
+    """Read op -> 4 recurrence ops -> stacked materialise op, backward through torch autograd.
+
+    fused_open: the read and the materialisation's use of X0 go through ops.read_with_residual, whose
+    backward writes dX0 = G_L + R^T gZ0 in one local_read_add pass."""
     B, G, C, L = 2, 16, 64, 4
     d = cfg(B, G, C, L, seed=3, grads=True)
     t = lambda a: dev(a).requires_grad_(True)  # noqa: E731
-    x0, alpha = t(d["x0"]), t(d["alpha"])
+    x0_leaf, alpha = t(d["x0"]), t(d["alpha"])
     betas, dzs = t(d["beta"]), [t(z) for z in d["dz"]]
-    z = ops.local_write_traceable(x0, alpha)
+    if fused_open:
+        x0, z = ops.read_with_residual(x0_leaf, alpha)
+    else:
+        x0, z = x0_leaf, ops.local_write_traceable(x0_leaf, alpha)
     zs = [z]
     for l in range(L):
         gam = (alpha * betas[l]).sum(-1)
@@ -161,11 +168,27 @@ def test_interface_autograd_matches_closed_form_fp32(coracle):
     loss = (xl * dev(d["grad_xl"])).sum() + sum((zs[l] * dev(d["grad_z"][l])).sum() for l in range(L))
     loss.backward()
     ref = O.interface_bwd_np(d["x0"], d["alpha"], list(d["dz"]), list(d["beta"]), d["grad_xl"], list(d["grad_z"]), G)
-    assert_f32(host(x0.grad), ref["x0"], what="dX0")
+    assert_f32(host(x0_leaf.grad), ref["x0"], what="dX0")
     assert_f32(host(alpha.grad), ref["alpha"], what="dalpha")
     for l in range(L):
         assert_f32(host(dzs[l].grad), ref["dz"][l], what=f"d dZ_{l}")
         assert_f32(host(betas.grad[l]), ref["beta"][l], what=f"dbeta_{l}")
+
+
+def test_read_add_op_and_backward_bf16(coracle):
+    """jit_thc::local_read_add_traceable: x + R^T z in one pass, and its autograd (grad_x = grad_out)."""
+    B, G, C = 4, 16, 768
+    d = cfg(B, G, C, 1, seed=5, grads=True)
+    x, z = dev(d["x0"], BF16), dev(d["dz"][0], BF16)
+    w = dev(d["beta"][0]).requires_grad_(True)
+    zr, xr = z.clone().requires_grad_(True), x.clone().requires_grad_(True)
+    out = ops.local_read_add_traceable(zr, w, xr)
+    assert_bf16(host(out), coracle.Cwrite(host(x), [host(z)], [d["beta"][0]]), what="x + R^T z")
+    g = dev(d["grad_xl"], BF16)
+    out.backward(g)
+    assert torch.equal(xr.grad, g)
+    assert_bf16(host(zr.grad), coracle.Cread(host(g), d["beta"][0], G), what="grad z = R g")
+    assert_f32(host(w.grad), coracle.Cweight_grad(host(g), [host(z)], G)[0], tol=1e-5, what="grad w")
 
 
 def test_recurrence_backward(coracle):

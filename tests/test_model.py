@@ -50,6 +50,7 @@ def conv_interface(model, form="conv"):
         return cells.reshape(dz.shape[0], g, g, s, s, c).permute(0, 1, 3, 2, 4, 5).reshape(dz.shape[0], g * s, g * s, c)
 
     model.shared_read.read = read
+    model.shared_read.read_with_residual = lambda x: (x, read(x))
     for blk in model.blocks:
         blk.write.write_add = lambda x_hi, dz, b=blk: x_hi + write(dz, b.write.beta(dtype=dz.dtype))
 
