@@ -145,6 +145,7 @@ def eager_interface(model, torch):
     model.shared_read.read_with_residual = lambda x: (x, read(x))
     for blk in model.blocks:
         blk.lazy_workspace_update = lambda z, dz, sr, b=blk: z + b.write.gamma_from_alpha(sr.alpha(dtype=dz.dtype))[None, None, :] * dz
+        blk.lazy_workspace_step = lambda z, dz, sr, b=blk: (b.lazy_workspace_update(z, dz, sr), dz)
 
     def final(x0, dz_list):
         x = x0
@@ -224,11 +225,12 @@ def interface_train(args, torch, dev, ops):
     def forward():
         x0v, z = ops.read_with_residual(x0, alpha.to(bf16))  # as the model's forward_lazy
         gam = ops.lazy_gamma_stack(alpha.to(bf16), torch.stack([b.to(bf16) for b in betas]))
-        zs = [z]
+        zs, dzv = [z], []
         for l in range(L):
-            z = ops.lazy_workspace_update(z, dzs[l], gam[l])
+            z, d = ops.lazy_workspace_step(z, dzs[l], gam[l])  # as the model's forward_lazy
             zs.append(z)
-        xl = ops.final_accumulate_b4_12_traceable(x0v, *dzs, *betas) if L == 12 else None
+            dzv.append(d)
+        xl = ops.final_accumulate_b4_12_traceable(x0v, *dzv, *betas) if L == 12 else None
         return xl, zs[:L]
 
     leaves = [x0, alpha] + betas + dzs

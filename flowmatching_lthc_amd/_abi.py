@@ -68,7 +68,7 @@ def load() -> ctypes.CDLL:
         "lthc_weight_grad": [vp, pp, ci, vp, i64, i64, i64, i64, ci, vp, sz, vp],
         "lthc_gamma": [vp, pp, ci, vp, ci, i64, i64, ci, vp],
         "lthc_recur_fwd": [vp, vp, ci, vp, ci, vp, i64, i64, vp],
-        "lthc_recur_bwd": [vp, vp, ci, vp, ci, vp, vp, i64, i64, vp, sz, vp],
+        "lthc_recur_bwd": [vp, vp, vp, ci, vp, ci, vp, vp, i64, i64, vp, sz, vp],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)

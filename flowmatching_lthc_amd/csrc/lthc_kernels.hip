@@ -859,10 +859,12 @@ __global__ __launch_bounds__(256) void recur_fwd_kernel(const void* __restrict__
   }
 }
 
-// RECURRENCE BACKWARD: gdz = gamma * g; partial[4*by + lane_row, c] = sum g*dz
-// over the rows the thread visits.  Grid and row order as recur_fwd_kernel.
-template <int DT, typename Off>
+// RECURRENCE BACKWARD: gdz = gamma * g (+ gadd, HAS_ADD); partial[4*by + lane_row, c]
+// = sum g*dz over the rows the thread visits.  Grid and row order as
+// recur_fwd_kernel.
+template <int DT, typename Off, bool HAS_ADD>
 __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__ g, const void* __restrict__ dz,
+                                                        const void* __restrict__ gadd,
                                                         const void* __restrict__ gamma, int gdt,
                                                         void* __restrict__ gdz, float* __restrict__ partial,
                                                         int64_t rows, int C) {
@@ -877,7 +879,7 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
   const int64_t re = rows;
   const int64_t S = static_cast<int64_t>(4 * kRU) * gridDim.y;
   for (int64_t r0 = static_cast<int64_t>(blockIdx.y) * 4 * kRU + (t >> 6); r0 < re; r0 += S) {
-    Raw<DT, 4> ar[kRU], dr[kRU];
+    Raw<DT, 4> ar[kRU], dr[kRU], xr[HAS_ADD ? kRU : 1];
     Off off[kRU];
 #pragma unroll
     for (int u = 0; u < kRU; ++u) {
@@ -885,6 +887,7 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
       off[u] = static_cast<Off>((r * C + c0) * ES);
       load_at<DT, 4, true>(g, off[u], ar[u]);
       load_at<DT, 4, true>(dz, off[u], dr[u]);
+      if constexpr (HAS_ADD) load_at<DT, 4, true>(gadd, off[u], xr[u]);
     }
     LTHC_PHASE_BARRIER();
 #pragma unroll
@@ -893,11 +896,16 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
         float a[4], d[4], o4[4];
         unpack_raw<DT, 4>(ar[u], a);
         unpack_raw<DT, 4>(dr[u], d);
+        if constexpr (HAS_ADD) {
+          unpack_raw<DT, 4>(xr[u], o4);
 #pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          o4[v] = gm[v] * a[v];
-          s[v] = fmaf(a[v], d[v], s[v]);
+          for (int v = 0; v < 4; ++v) o4[v] = fmaf(gm[v], a[v], o4[v]);
+        } else {
+#pragma unroll
+          for (int v = 0; v < 4; ++v) o4[v] = gm[v] * a[v];
         }
+#pragma unroll
+        for (int v = 0; v < 4; ++v) s[v] = fmaf(a[v], d[v], s[v]);
         store_at<DT, 4, true>(gdz, off[u], o4);
       }
     }
@@ -1347,7 +1355,7 @@ extern "C" {
 
 const char* lthc_last_error(void) { return g_last_error.c_str(); }
 
-int lthc_abi_version(void) { return 1; }
+int lthc_abi_version(void) { return 2; }
 
 int lthc_read_fwd(const void* x, int x_dtype, const void* alpha, int w_dtype, void* z, int64_t B, int64_t G, int64_t s,
                   int64_t C, void* stream) {
@@ -1511,8 +1519,9 @@ size_t lthc_recur_bwd_workspace_bytes(int64_t rows, int64_t C) {
   return static_cast<size_t>(recur_bwd_blocks_y(rows) * 4 * C) * sizeof(float);
 }
 
-int lthc_recur_bwd(const void* g, const void* dz, int x_dtype, const void* gamma, int g_dtype, void* gdz, float* ggamma,
-                   int64_t rows, int64_t C, void* workspace, size_t workspace_bytes, void* stream) {
+int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dtype, const void* gamma, int g_dtype,
+                   void* gdz, float* ggamma, int64_t rows, int64_t C, void* workspace, size_t workspace_bytes,
+                   void* stream) {
   static const char* fn = "lthc_recur_bwd";
   g_last_error.clear();
   if (rows < 0 || C <= 0 || C % 4 != 0 || C > (1 << 24)) return fail(LTHC_ERR_INVALID, fn, "rows >= 0 and C > 0, C % 4 == 0 required");
@@ -1526,6 +1535,8 @@ int lthc_recur_bwd(const void* g, const void* dz, int x_dtype, const void* gamma
   if (int rc = check_act(fn, g, x_dtype, "g")) return rc;
   if (int rc = check_act(fn, dz, x_dtype, "dz")) return rc;
   if (int rc = check_act(fn, gdz, x_dtype, "gdz")) return rc;
+  if (gdz_add != nullptr)
+    if (int rc = check_act(fn, gdz_add, x_dtype, "gdz_add")) return rc;
   const size_t need = lthc_recur_bwd_workspace_bytes(rows, C);
   if (workspace == nullptr || workspace_bytes < need)
     return fail(LTHC_ERR_INVALID, fn, "workspace smaller than lthc_recur_bwd_workspace_bytes()");
@@ -1536,8 +1547,12 @@ int lthc_recur_bwd(const void* g, const void* dz, int x_dtype, const void* gamma
   const bool off32 = fits32(rows * C * esize(x_dtype));
   dispatch_dtype(x_dtype, [&](auto d) {
     dispatch_off(off32, [&](auto o) {
-      recur_bwd_kernel<decltype(d)::value, typename decltype(o)::type>
-          <<<grid, 256, 0, st>>>(g, dz, gamma, g_dtype, gdz, partial, rows, static_cast<int>(C));
+      if (gdz_add != nullptr)
+        recur_bwd_kernel<decltype(d)::value, typename decltype(o)::type, true>
+            <<<grid, 256, 0, st>>>(g, dz, gdz_add, gamma, g_dtype, gdz, partial, rows, static_cast<int>(C));
+      else
+        recur_bwd_kernel<decltype(d)::value, typename decltype(o)::type, false>
+            <<<grid, 256, 0, st>>>(g, dz, nullptr, gamma, g_dtype, gdz, partial, rows, static_cast<int>(C));
     });
   });
   if (int rc = check_launch(fn)) return rc;

@@ -284,6 +284,14 @@ class SharedReadLocalTHCSharedAdaLNJiTBlock(nn.Module):
         gamma = self.write.gamma_from_alpha(shared_read.alpha(dtype=dz.dtype))
         return ops.lazy_workspace_update(z, dz, gamma)
 
+    def lazy_workspace_step(
+        self, z: torch.Tensor, dz: torch.Tensor, shared_read: SharedLocalRead
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        """(lazy_workspace_update(z, dz), dz) for the lazy forward, where dz is also materialised at the end;
+        the backward writes dz's whole gradient in one recurrence-backward pass (ops.lazy_workspace_step)."""
+        gamma = self.write.gamma_from_alpha(shared_read.alpha(dtype=dz.dtype))
+        return ops.lazy_workspace_step(z, dz, gamma)
+
 
 def migrate_lthc_state_dict_keys(state_dict: dict) -> dict:
     """Old checkpoint key names -> current ones (local_thc.py:41-61): the old code called the read 'write'."""
@@ -427,12 +435,15 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
 
     def forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         t6, t2 = self._conditioning(t, y)
+        # local_thc.py:1376-1385 (read once, one branch + recurrence per block, one materialisation).  The read
+        # and the recurrence steps are the fused-backward forms: same values, x0's and each dZ_l's gradient
+        # from one kernel instead of a kernel plus autograd's add.
         x0, z = self.shared_read.read_with_residual(self.x_embedder(x))
         dz_list = []
         for block in self.blocks:
             dz = block.branch_update(z, t6, self.workspace_rope)
+            z, dz = block.lazy_workspace_step(z, dz, self.shared_read)
             dz_list.append(dz)
-            z = block.lazy_workspace_update(z, dz, self.shared_read)
         return self._decode(self.final_accumulate_reference(x0, dz_list), t2)
 
     def forward_naive(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:

@@ -314,6 +314,7 @@ class _OpenInterface(torch.autograd.Function):
     def forward(ctx, x: Tensor, weight: Tensor):
         z = local_write_traceable(x, weight)
         ctx.save_for_backward(x, weight)
+        ctx.set_materialize_grads(False)  # an unused output's gradient arrives as None, not zeros
         return x.view_as(x), z
 
     @staticmethod
@@ -586,12 +587,18 @@ def _(z: Tensor, dz: Tensor, gamma: Tensor) -> Tensor:
 
 
 @torch.library.custom_op("jit_thc::lazy_workspace_update_backward", mutates_args=())
-def lazy_workspace_update_backward(grad: Tensor, dz: Tensor, gamma: Tensor) -> tuple[Tensor, Tensor]:
-    """(gamma * grad in grad.dtype, fp32 [C] sum over rows of grad * dz)."""
+def lazy_workspace_update_backward(
+    grad: Tensor, dz: Tensor, gamma: Tensor, gdz_add: Tensor | None = None
+) -> tuple[Tensor, Tensor]:
+    """(gamma * grad [+ gdz_add] in grad.dtype, fp32 [C] sum over rows of grad * dz)."""
     _on_gpu(grad, dz, gamma)
     c = _check_recur(grad, dz, gamma)
     grad = _prep(grad)
     (dz,) = _same_dtype(grad, [_prep(dz)])
+    if gdz_add is not None:
+        if gdz_add.shape != grad.shape:
+            raise ValueError(f"gdz_add {tuple(gdz_add.shape)} must match grad {tuple(grad.shape)}")
+        (gdz_add,) = _same_dtype(grad, [_prep(gdz_add)])
     gamma = _prep(gamma)
     rows = grad.numel() // c
     gdz = torch.empty_like(grad)
@@ -599,15 +606,15 @@ def lazy_workspace_update_backward(grad: Tensor, dz: Tensor, gamma: Tensor) -> t
     ws = torch.empty((max(_abi.recur_bwd_workspace_bytes(rows, c), 16),), device=grad.device, dtype=torch.uint8)
     with _on_device(grad):
         rc = _abi.load().lthc_recur_bwd(
-            grad.data_ptr(), dz.data_ptr(), _abi.code(grad), gamma.data_ptr(), _abi.code(gamma), gdz.data_ptr(),
-            ggamma.data_ptr(), rows, c, ws.data_ptr(), ws.numel(), _abi.stream_of(grad),
+            grad.data_ptr(), dz.data_ptr(), _abi.ptr(gdz_add), _abi.code(grad), gamma.data_ptr(), _abi.code(gamma),
+            gdz.data_ptr(), ggamma.data_ptr(), rows, c, ws.data_ptr(), ws.numel(), _abi.stream_of(grad),
         )  # fmt: skip
     _abi.check(rc, "lthc_recur_bwd")
     return gdz, ggamma
 
 
 @lazy_workspace_update_backward.register_fake
-def _(grad: Tensor, dz: Tensor, gamma: Tensor):
+def _(grad: Tensor, dz: Tensor, gamma: Tensor, gdz_add: Tensor | None = None):
     return torch.empty_like(grad), grad.new_empty((grad.shape[-1],), dtype=torch.float32)
 
 
@@ -630,6 +637,48 @@ def _backward_recur(ctx, grad):
 
 
 torch.library.register_autograd(lazy_workspace_update, _backward_recur, setup_context=_setup_recur_ctx)
+
+
+class _RecurStep(torch.autograd.Function):
+    """(Z_{l+1} = Z_l + gamma * dZ_l, dZ_l) as one autograd node.
+
+    In the lazy forward dZ_l feeds both the recurrence and the final
+    materialisation, so autograd would add the two gradients of dZ_l in a
+    separate pass; here the node receives both and one recurrence-backward
+    launch writes gamma * g + (materialisation's gradient).
+    """
+
+    @staticmethod
+    def forward(ctx, z: Tensor, dz: Tensor, gamma: Tensor):
+        zn = lazy_workspace_update(z, dz, gamma)
+        ctx.save_for_backward(dz, gamma)
+        ctx.z_dtype = z.dtype
+        ctx.set_materialize_grads(False)  # an unused Z_{l+1} (the last step's) skips the recurrence backward
+        return zn, dz.view_as(dz)
+
+    @staticmethod
+    def backward(ctx, grad_zn: Tensor | None, grad_dz: Tensor | None):
+        dz, gamma = ctx.saved_tensors
+        need = ctx.needs_input_grad
+        if grad_zn is None:
+            return None, grad_dz, None
+        grad_z = grad_zn.to(ctx.z_dtype) if need[0] else None
+        gdz = gg = None
+        if need[1] or need[2]:
+            add = grad_dz if need[1] else None
+            gdz, gg = lazy_workspace_update_backward(grad_zn, dz, gamma, add)
+            gdz = gdz.to(dz.dtype) if need[1] else None
+            gg = gg.to(gamma.dtype) if need[2] else None
+        return grad_z, gdz, gg
+
+
+def lazy_workspace_step(z: Tensor, dz: Tensor, gamma: Tensor) -> tuple[Tensor, Tensor]:
+    """(lazy_workspace_update(z, dz, gamma), dz) with a fused backward for a later consumer of dz.
+
+    Values are those of the separate uses; the backward of dz is gamma * g_next plus the later
+    consumer's gradient, written by one recurrence-backward launch instead of a launch and an add.
+    """
+    return _RecurStep.apply(z, dz, gamma)
 
 
 # ---------------------------------------------------------------------------

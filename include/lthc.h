@@ -144,13 +144,17 @@ int lthc_recur_fwd(const void* z, const void* dz, int x_dtype, const void* gamma
 
 /*
  * RECURRENCE BACKWARD (given g = dL/dz_next)
- *   gdz[r,c]   = gamma[c] * g[r,c]                 (x_dtype)
- *   ggamma[c]  = sum_r g[r,c] * dz[r,c]            (fp32, deterministic)
- * dL/dz = g itself, as in eager autograd of local_thc.py:1328.
+ *   gdz[r,c]   = gamma[c] * g[r,c] (+ gdz_add[r,c])   (x_dtype; one rounding)
+ *   ggamma[c]  = sum_r g[r,c] * dz[r,c]               (fp32, deterministic)
+ * dL/dz = g itself, as in eager autograd of local_thc.py:1328.  gdz_add may
+ * be NULL; when given it is added before the single rounding, so a caller
+ * whose dz also feeds the final materialisation gets the whole gradient of
+ * dz (that use's contribution, from lthc_read_multi_fwd, plus this one) in
+ * one pass instead of a separate add.
  */
 size_t lthc_recur_bwd_workspace_bytes(int64_t rows, int64_t C);
-int lthc_recur_bwd(const void* g, const void* dz, int x_dtype, const void* gamma, int g_dtype,
-                   void* gdz, float* ggamma, int64_t rows, int64_t C,
+int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dtype, const void* gamma,
+                   int g_dtype, void* gdz, float* ggamma, int64_t rows, int64_t C,
                    void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus

@@ -82,15 +82,15 @@ def recur(z: torch.Tensor, dz: torch.Tensor, gam: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def recur_bwd(gr: torch.Tensor, dz: torch.Tensor, gam: torch.Tensor):
+def recur_bwd(gr: torch.Tensor, dz: torch.Tensor, gam: torch.Tensor, add: torch.Tensor | None = None):
     c = gr.shape[-1]
     rows = gr.numel() // c
     gdz = torch.empty_like(gr)
     gg = torch.empty((c,), device=gr.device, dtype=torch.float32)
     ws = torch.empty((max(_abi.recur_bwd_workspace_bytes(rows, c), 16),), device=gr.device, dtype=torch.uint8)
     rc = _lib().lthc_recur_bwd(
-        gr.data_ptr(), dz.data_ptr(), _abi.code(gr), gam.data_ptr(), _abi.code(gam), gdz.data_ptr(), gg.data_ptr(), rows, c,
-        ws.data_ptr(), ws.numel(), _stream(),
+        gr.data_ptr(), dz.data_ptr(), _abi.ptr(add), _abi.code(gr), gam.data_ptr(), _abi.code(gam), gdz.data_ptr(),
+        gg.data_ptr(), rows, c, ws.data_ptr(), ws.numel(), _stream(),
     )  # fmt: skip
     _abi.check(rc, "lthc_recur_bwd")
     return gdz, gg

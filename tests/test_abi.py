@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert sorted(_abi.EXPORTS) == names
-    assert lib.lthc_abi_version() == 1
+    assert lib.lthc_abi_version() == 2
 
 
 def _err(rc):

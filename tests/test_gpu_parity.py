@@ -148,8 +148,9 @@ def test_config3_read_backward_bf16(coracle):
 def test_interface_autograd_matches_closed_form_fp32(coracle, fused_open):
     """Read op -> 4 recurrence ops -> stacked materialise op, backward through torch autograd.
 
-    fused_open: the read and the materialisation's use of X0 go through ops.read_with_residual, whose
-    backward writes dX0 = G_L + R^T gZ0 in one local_read_add pass."""
+    fused_open: the model's forward_lazy form -- the read and the materialisation's use of X0 go through
+    ops.read_with_residual (dX0 = G_L + R^T gZ0 in one local_read_add pass) and every recurrence step
+    through ops.lazy_workspace_step (dZ_l's two gradients summed inside the recurrence backward)."""
     B, G, C, L = 2, 16, 64, 4
     d = cfg(B, G, C, L, seed=3, grads=True)
     t = lambda a: dev(a).requires_grad_(True)  # noqa: E731
@@ -159,12 +160,16 @@ def test_interface_autograd_matches_closed_form_fp32(coracle, fused_open):
         x0, z = ops.read_with_residual(x0_leaf, alpha)
     else:
         x0, z = x0_leaf, ops.local_write_traceable(x0_leaf, alpha)
-    zs = [z]
+    zs, dzm = [z], []
     for l in range(L):
         gam = (alpha * betas[l]).sum(-1)
-        z = ops.lazy_workspace_update(z, dzs[l], gam)
+        if fused_open:
+            z, dz_m = ops.lazy_workspace_step(z, dzs[l], gam)
+        else:
+            z, dz_m = ops.lazy_workspace_update(z, dzs[l], gam), dzs[l]
         zs.append(z)
-    xl = ops.final_accumulate_b4_traceable(x0, torch.stack(dzs), betas)
+        dzm.append(dz_m)
+    xl = ops.final_accumulate_b4_traceable(x0, torch.stack(dzm), betas)
     loss = (xl * dev(d["grad_xl"])).sum() + sum((zs[l] * dev(d["grad_z"][l])).sum() for l in range(L))
     loss.backward()
     ref = O.interface_bwd_np(d["x0"], d["alpha"], list(d["dz"]), list(d["beta"]), d["grad_xl"], list(d["grad_z"]), G)
@@ -199,6 +204,11 @@ def test_recurrence_backward(coracle):
     rgdz, rgg = coracle.Crecur_bwd(host(g), host(dz), host(gam))
     assert_bf16(host(gdz), rgdz, what="gamma * g")
     assert_f32(host(gg), rgg, tol=1e-5, what="ggamma")
+    # with the accumulate input: gamma * g + add, one rounding
+    add = dev(d["grad_z"][1], BF16)
+    gdz2, gg2 = capi.recur_bwd(g, dz, gam, add)
+    assert_bf16(host(gdz2), rgdz.astype(np.float64) + host(add), what="gamma * g + add")
+    assert torch.equal(gg2, gg)
 
 
 # ---------------------------------------------------------------------------

@@ -58,6 +58,7 @@ def conv_interface(model, form="conv"):
             return z + b.write.gamma_from_alpha(shared_read.alpha(dtype=dz.dtype))[None, None, :] * dz
 
         blk.lazy_workspace_update = lazy
+        blk.lazy_workspace_step = lambda z, dz, shared_read, f=lazy: (f(z, dz, shared_read), dz)
 
     def final(x0, dz_list):
         x = x0
