@@ -53,6 +53,7 @@ def parse_args():
     p.add_argument("--no-model", action="store_true", help="skip the LTHC-B/4 forward leg")
     p.add_argument("--train-batch", type=int, default=64, help="batch of the interface fwd+bwd leg (configuration 3)")
     p.add_argument("--no-train", action="store_true", help="skip the interface fwd+bwd leg")
+    p.add_argument("--no-configs", action="store_true", help="skip the BASELINE configuration 2 and 5 legs")
     p.add_argument(
         "--profile",
         choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model", "train"],
@@ -202,7 +203,68 @@ def model_forward(args, torch, dev):
     }
 
 
-def interface_train(args, torch, dev, ops):
+def interface_forward(args, torch, dev, ops, B, G, C, L):
+    """The interface forward step (read, gamma stack, L recurrence steps, materialise) at one configuration,
+    captured as a HIP graph per input set (two sets) and replayed; returns ms per step and GB/s of the per-op
+    compulsory bytes."""
+    H = 4 * G
+    bf16 = torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(7)
+    alpha = torch.randn((C, 16), generator=gen, device=dev) * 0.01 + 1.0 / 16.0
+    beta_stack = torch.randn((L, C, 16), generator=gen, device=dev) * 0.02
+    betas = list(beta_stack.unbind(0))
+    sets = []
+    for _ in range(2):
+        x0 = torch.randn((B, H, H, C), generator=gen, device=dev).to(bf16)
+        dzs = [(torch.randn((B, G * G, C), generator=gen, device=dev) * 0.02).to(bf16) for _ in range(L)]
+        sets.append((x0, dzs, torch.stack(dzs) if L != 12 else None))
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        x0, dzs, stack = sets[i % 2]
+        z = ops.local_write_traceable(x0, alpha)
+        gam = ops.lazy_gamma_stack(alpha, beta_stack)
+        for l in range(L):
+            z = ops.lazy_workspace_update(z, dzs[l], gam[l])
+        if L == 12:
+            xl = ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas)
+        else:  # the dZ stack is an input here, as the transformer would write it
+            xl = ops.final_accumulate_b4_traceable(x0, stack, beta_stack)
+        return z, xl
+
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for i in range(2):
+            step(i)
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graphs = []
+    for i in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(i)
+        graphs.append(g)
+    for i in range(max(2, args.warmup)):
+        graphs[i % 2].replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        graphs[i % 2].replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    nbytes = algorithmic_bytes(B, G, C, L)["total"]
+    return {
+        "B": B, "high_grid": H, "workspace_grid": G, "C": C, "L": L,
+        "ms_per_step": round(ms, 4),
+        "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1),
+        "pct_of_peak_hbm": round(100.0 * nbytes / (ms * 1e-3) / PEAK_HBM, 2),
+    }
+
+
+def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label="configuration 3"):
     """the interface forward + autograd backward at the training shape (B=64, bf16).
 
     X0, alpha, the 12 beta_l and the 12 dZ_l are leaves that require grad; the upstream gradients are
@@ -210,7 +272,10 @@ def interface_train(args, torch, dev, ops):
     the branches.  One step = read (the fused-open form of the model's forward_lazy), gamma stack, 12
     recurrence steps, 12-pointer materialise, then torch.autograd.grad over (X_L, Z_0..Z_11) -- every backward
     kernel of the interface plus autograd's own gradient accumulation (adds), as in training."""
-    B, G, C, L = args.train_batch, args.grid, args.channels, args.depth
+    B = args.train_batch if B is None else B
+    G = args.grid if G is None else G
+    C = args.channels if C is None else C
+    L = args.depth if L is None else L
     H = 4 * G
     bf16 = torch.bfloat16
     gen = torch.Generator(device=dev).manual_seed(3)
@@ -230,7 +295,10 @@ def interface_train(args, torch, dev, ops):
             z, d = ops.lazy_workspace_step(z, dzs[l], gam[l])  # as the model's forward_lazy
             zs.append(z)
             dzv.append(d)
-        xl = ops.final_accumulate_b4_12_traceable(x0v, *dzv, *betas) if L == 12 else None
+        if L == 12:
+            xl = ops.final_accumulate_b4_12_traceable(x0v, *dzv, *betas)
+        else:  # the base-class materialisation (stacked op)
+            xl = ops.final_accumulate_b4_traceable(x0v, torch.stack(dzv), torch.stack(betas))
         return xl, zs[:L]
 
     leaves = [x0, alpha] + betas + dzs
@@ -291,7 +359,7 @@ def interface_train(args, torch, dev, ops):
     fwd_ms, step_ms = (graph_fwd, graph_step) if graph_error is None else (eager_fwd, eager_step)
     bwd_ms = step_ms - fwd_ms
     return {
-        "workload": "interface fwd + autograd bwd, configuration 3 (B=64, C=768, L=12, bf16, fp32 weights)",
+        "workload": f"interface fwd + autograd bwd, {label} (B={B}, {H}x{H}/{G}x{G}, C={C}, L={L}, bf16, fp32 weights)",
         "batch": B,
         "steps": args.steps,
         "timing": "HIP graph replays (forward alone; forward + autograd.grad), eager for comparison"
@@ -452,10 +520,23 @@ def main():
     mat_achieved = nbytes["materialise"] / (mat_ms * 1e-3)
     traffic = pmc_traffic()
 
-    del sets, graphs
+    # release every tensor and graph pool of the main measurement before the other legs
+    outs = ref = None
+    del sets, graphs, outs, ref, mat_events
+    import gc
+
+    gc.collect()
+    torch.cuda.synchronize()
     torch.cuda.empty_cache()
     model_fwd = None if args.no_model else model_forward(args, torch, dev)
     train = None if args.no_train else interface_train(args, torch, dev, ops)
+    configs = None
+    if not args.no_configs:
+        configs = {
+            "config2_fwd": interface_forward(args, torch, dev, ops, 32, 16, 768, 12),
+            "config5_fwd": interface_forward(args, torch, dev, ops, 32, 32, 1024, 24),
+            "config5_train": interface_train(args, torch, dev, ops, 32, 32, 1024, 24, label="configuration 5"),
+        }
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -501,6 +582,7 @@ def main():
         "cpu_baseline": cpu,
         "model_fwd": model_fwd,
         "interface_train": train,
+        "configs": configs,
         "extra": {
             "eager_ms_per_step": round(eager_ms, 4),
             "graph_ms_per_step": None if graph_ms is None else round(graph_ms, 4),

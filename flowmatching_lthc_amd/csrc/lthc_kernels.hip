@@ -320,57 +320,63 @@ __global__ __launch_bounds__(kBlock) void read_fwd_kernel(const void* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// WHOLE-CELL MATERIALISE / WRITE (depth <= 12, tensors below 4 GiB):
+// WHOLE-CELL MATERIALISE / WRITE (depth <= 24, tensors below 4 GiB):
 // out[cell,k,c] = base[cell,k,c] + sum_l beta_l[c,k] dz_l[cell,c]
-// Thread = CPT channels x all 16 taps of a cell, so each dz run is loaded by
-// exactly one lane (no re-requests of the same line by several waves), and
-// its LMAX x CPT x 16 write weights stay in VGPRs.  Block = 256 threads = one
-// slab of 256*CPT channels; a wavefront access is a contiguous 64*CPT-element
-// run of one tap.  Cells are visited grid-stride with gridDim.x % G == 0 and
-// gridDim.x * gridDim.y no larger than the resident block count, so the whole
-// grid sweeps one compact window of cells at a time with no tail round.
-// When L < LMAX (EXACT == false) the padding layers load layer 0 and
-// contribute a selected 0.
+// Thread = CPT channels x the 16 / TG taps of its tap group (TG = 1: the
+// whole cell; TG = 2: tap rows 0-1 or 2-3, for depths whose weights would
+// not fit otherwise); its LMAX x CPT x (16 / TG) write weights stay in VGPRs.
+// Block = TG groups x 256 / TG lanes, one slab of 256 * CPT / TG channels; a
+// wavefront lies in one tap group, so each dz run is requested once per tap
+// group (once per cell when TG = 1) and every wavefront access is a
+// contiguous 64 * CPT-element run of one tap.  Cells are visited grid-stride
+// with gridDim.x % G == 0 and gridDim.x * gridDim.y no larger than the
+// resident block count, so the whole grid sweeps one compact window of cells
+// at a time with no tail round.  When L < LMAX (EXACT == false) the padding
+// layers load layer 0 and contribute a selected 0.
 // Accumulation: acc = base, acc = fma(beta_l, dz_l, acc) for l = 0..L-1
 // (local_thc_triton_kernels.py:367-403).  Base reads and output writes are
 // streaming (non-temporal).
 // ---------------------------------------------------------------------------
-template <int DT, int WDT, int LMAX, int CPT, bool HAS_BASE, bool EXACT>
+template <int DT, int WDT, int LMAX, int CPT, int TG, bool HAS_BASE, bool EXACT>
 __global__ __launch_bounds__(kBlock) void cell_mat_kernel(const void* __restrict__ base, PtrPack dz, PtrPack beta,
                                                           void* __restrict__ out, int L, uint32_t ncells, int G,
                                                           int C) {
   constexpr int ES = Fmt<DT>::bytes;
-  const int c0 = (blockIdx.y * kBlock + threadIdx.x) * CPT;
+  constexpr int TPT = kK / TG;
+  constexpr int QL = kBlock / TG;
+  const int g = TG == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x / QL);  // wave-uniform tap group
+  const int c0 = (blockIdx.y * QL + (threadIdx.x - g * QL)) * CPT;
+  const int tap0 = g * TPT;
   uint32_t cell = blockIdx.x;
   if (c0 >= C || cell >= ncells) return;
-  float bw[LMAX][CPT][kK];
+  float bw[LMAX][CPT][TPT];
 #pragma unroll
   for (int l = 0; l < LMAX; ++l) {
     const void* bp = beta.p[(EXACT || l < L) ? l : 0];
 #pragma unroll
-    for (int v = 0; v < CPT; ++v) load_wvec<WDT, kK>(bp, static_cast<int64_t>(c0 + v) * kK, bw[l][v]);
+    for (int v = 0; v < CPT; ++v) load_wvec<WDT, TPT>(bp, static_cast<int64_t>(c0 + v) * kK + tap0, bw[l][v]);
   }
   const uint32_t tap_b = C * ES;
   const uint32_t row_b = G * kS * tap_b;
   const uint32_t P = gridDim.x;
   const uint32_t step_x = (P / G) * kS * row_b;
   const uint32_t step_z = P * tap_b;
-  uint32_t xo = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES);
+  uint32_t xo = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES) + (tap0 / kS) * row_b;
   uint32_t zo = (cell * C + c0) * ES;
   for (; cell < ncells; cell += P, xo += step_x, zo += step_z) {
-    Raw<DT, CPT> xr[kK];
+    Raw<DT, CPT> xr[TPT];
     Raw<DT, CPT> dr[LMAX];
     if constexpr (HAS_BASE) {
 #pragma unroll
-      for (int k = 0; k < kK; ++k) load_at<DT, CPT, true>(base, xo + (k / kS) * row_b + (k % kS) * tap_b, xr[k]);
+      for (int k = 0; k < TPT; ++k) load_at<DT, CPT, true>(base, xo + (k / kS) * row_b + (k % kS) * tap_b, xr[k]);
     }
 #pragma unroll
     for (int l = 0; l < LMAX; ++l) load_at<DT, CPT>(dz.p[(EXACT || l < L) ? l : 0], zo, dr[l]);
     LTHC_PHASE_BARRIER();
 
-    float acc[kK][CPT];
+    float acc[TPT][CPT];
 #pragma unroll
-    for (int k = 0; k < kK; ++k) {
+    for (int k = 0; k < TPT; ++k) {
       if constexpr (HAS_BASE) {
         unpack_raw<DT, CPT>(xr[k], acc[k]);
       } else {
@@ -388,12 +394,12 @@ __global__ __launch_bounds__(kBlock) void cell_mat_kernel(const void* __restrict
         for (int v = 0; v < CPT; ++v) d[v] = live ? d[v] : 0.f;
       }
 #pragma unroll
-      for (int k = 0; k < kK; ++k)
+      for (int k = 0; k < TPT; ++k)
 #pragma unroll
         for (int v = 0; v < CPT; ++v) acc[k][v] = fmaf(bw[l][v][k], d[v], acc[k][v]);
     }
 #pragma unroll
-    for (int k = 0; k < kK; ++k) store_at<DT, CPT, true>(out, xo + (k / kS) * row_b + (k % kS) * tap_b, acc[k]);
+    for (int k = 0; k < TPT; ++k) store_at<DT, CPT, true>(out, xo + (k / kS) * row_b + (k % kS) * tap_b, acc[k]);
   }
 }
 
@@ -632,26 +638,33 @@ __global__ __launch_bounds__(kBlock) void wgrad_partial_kernel(const void* __res
 // Zero fill by a kernel rather than hipMemsetAsync, so that callers may
 // capture these launches in a HIP graph.
 // ---------------------------------------------------------------------------
-// WHOLE-CELL MULTI-WEIGHT READ (depth <= 12, tensors below 4 GiB):
+// WHOLE-CELL MULTI-WEIGHT READ (depth <= 24, tensors below 4 GiB):
 //   out_l[cell,c] = sum_k w_l[c,k] g[cell,k,c]
-// Thread = CPT channels x all 16 taps x all LMAX layers, so each g run is
-// loaded by exactly one lane; the LMAX x CPT x 16 weights stay in VGPRs.
-// Grid and cell order as cell_mat_kernel.  Padding layers (l >= L) load
-// layer 0's weights and are never stored.
+// Thread = CPT channels x all 16 taps x the LMAX / LG layers of its layer
+// group; the weights stay in VGPRs.  Block = LG groups x 256 / LG lanes (a
+// wavefront lies in one group), so each g run is loaded once per layer group
+// (once per cell when LG = 1).  Grid and cell order as cell_mat_kernel.
+// Padding layers (l >= L) load layer 0's weights and are never stored.
 // Accumulation order k = 0..15 (local_thc_triton_kernels.py:580-592).
 // ---------------------------------------------------------------------------
-template <int DT, int WDT, int LMAX, int CPT>
+template <int DT, int WDT, int LMAX, int CPT, int LG>
 __global__ __launch_bounds__(kBlock) void cell_read_multi_kernel(const void* __restrict__ g, PtrPack w, PtrPack out,
                                                                  int L, uint32_t ncells, int G, int C) {
   constexpr int ES = Fmt<DT>::bytes;
-  const int c0 = (blockIdx.y * kBlock + threadIdx.x) * CPT;
+  constexpr int LPG = LMAX / LG;
+  constexpr int QL = kBlock / LG;
+  // the layer group is wave-uniform (QL >= 64): keep it scalar so out.p[l0 + i] is a scalar kernarg load
+  const int lg = LG == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x / QL);
+  const int c0 = (blockIdx.y * QL + (threadIdx.x - lg * QL)) * CPT;
+  const int l0 = lg * LPG;
   uint32_t cell = blockIdx.x;
-  if (c0 >= C || cell >= ncells) return;
-  float wr[LMAX][CPT][kK];
+  if (c0 >= C || cell >= ncells || l0 >= L) return;
+  float wr[LPG][CPT][kK];
 #pragma unroll
-  for (int l = 0; l < LMAX; ++l)
+  for (int i = 0; i < LPG; ++i)
 #pragma unroll
-    for (int v = 0; v < CPT; ++v) load_wvec<WDT, kK>(w.p[l < L ? l : 0], static_cast<int64_t>(c0 + v) * kK, wr[l][v]);
+    for (int v = 0; v < CPT; ++v)
+      load_wvec<WDT, kK>(w.p[l0 + i < L ? l0 + i : 0], static_cast<int64_t>(c0 + v) * kK, wr[i][v]);
   const uint32_t tap_b = C * ES;
   const uint32_t row_b = G * kS * tap_b;
   const uint32_t P = gridDim.x;
@@ -664,67 +677,72 @@ __global__ __launch_bounds__(kBlock) void cell_read_multi_kernel(const void* __r
 #pragma unroll
     for (int k = 0; k < kK; ++k) load_at<DT, CPT, true>(g, go + (k / kS) * row_b + (k % kS) * tap_b, gr[k]);
     LTHC_PHASE_BARRIER();
-    float acc[LMAX][CPT];
+    float acc[LPG][CPT];
 #pragma unroll
-    for (int l = 0; l < LMAX; ++l)
+    for (int i = 0; i < LPG; ++i)
 #pragma unroll
-      for (int v = 0; v < CPT; ++v) acc[l][v] = 0.f;
+      for (int v = 0; v < CPT; ++v) acc[i][v] = 0.f;
 #pragma unroll
     for (int k = 0; k < kK; ++k) {
       float gv[CPT];
       unpack_raw<DT, CPT>(gr[k], gv);
 #pragma unroll
-      for (int l = 0; l < LMAX; ++l)
+      for (int i = 0; i < LPG; ++i)
 #pragma unroll
-        for (int v = 0; v < CPT; ++v) acc[l][v] = fmaf(gv[v], wr[l][v][k], acc[l][v]);
+        for (int v = 0; v < CPT; ++v) acc[i][v] = fmaf(gv[v], wr[i][v][k], acc[i][v]);
     }
 #pragma unroll
-    for (int l = 0; l < LMAX; ++l)
-      if (l < L) store_at<DT, CPT>(const_cast<void*>(out.p[l]), zo, acc[l]);
+    for (int i = 0; i < LPG; ++i)
+      if (l0 + i < L) store_at<DT, CPT>(const_cast<void*>(out.p[l0 + i]), zo, acc[i]);
   }
 }
 
 // ---------------------------------------------------------------------------
-// WHOLE-CELL CELL WEIGHT GRADIENT, stage 1 (depth <= 12, tensors below 4 GiB):
+// WHOLE-CELL CELL WEIGHT GRADIENT, stage 1 (depth <= 24, tensors below 4 GiB):
 //   partial[bx, l, c, k] = sum_{cells of block column bx} high[cell,k,c] low_l[cell,c]
-// Thread = CPT channels x all 16 taps; its LMAX x CPT x 16 fp32 accumulators
-// stay in VGPRs over the block column's grid-stride cells (each low run is
-// loaded by one lane).  Every block writes its partial slot, zeros included.
-// Padding layers accumulate layer 0 and are never written.
+// Thread = CPT channels x the 16 / TG taps of its tap group (as
+// cell_mat_kernel); its LMAX x CPT x (16 / TG) fp32 accumulators stay in
+// VGPRs over the block column's grid-stride cells.  Every block writes its
+// partial slot, zeros included.  Padding layers accumulate layer 0 and are
+// never written.
 // ---------------------------------------------------------------------------
-template <int DT, int LMAX, int CPT>
+template <int DT, int LMAX, int CPT, int TG>
 __global__ __launch_bounds__(kBlock) void cell_wgrad_kernel(const void* __restrict__ high, PtrPack low,
                                                             float* __restrict__ partial, int L, uint32_t ncells, int G,
                                                             int C) {
   constexpr int ES = Fmt<DT>::bytes;
-  const int c0 = (blockIdx.y * kBlock + threadIdx.x) * CPT;
+  constexpr int TPT = kK / TG;
+  constexpr int QL = kBlock / TG;
+  const int g = TG == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x / QL);  // wave-uniform tap group
+  const int c0 = (blockIdx.y * QL + (threadIdx.x - g * QL)) * CPT;
+  const int tap0 = g * TPT;
   if (c0 >= C) return;
-  float acc[LMAX][CPT][kK];
+  float acc[LMAX][CPT][TPT];
 #pragma unroll
   for (int l = 0; l < LMAX; ++l)
 #pragma unroll
     for (int v = 0; v < CPT; ++v)
 #pragma unroll
-      for (int k = 0; k < kK; ++k) acc[l][v][k] = 0.f;
+      for (int k = 0; k < TPT; ++k) acc[l][v][k] = 0.f;
   const uint32_t tap_b = C * ES;
   const uint32_t row_b = G * kS * tap_b;
   const uint32_t P = gridDim.x;
   const uint32_t step_x = (P / G) * kS * row_b;
   const uint32_t step_z = P * tap_b;
   uint32_t cell = blockIdx.x;
-  uint32_t ho = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES);
+  uint32_t ho = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES) + (tap0 / kS) * row_b;
   uint32_t zo = (cell * C + c0) * ES;
   for (; cell < ncells; cell += P, ho += step_x, zo += step_z) {
-    Raw<DT, CPT> hr[kK];
+    Raw<DT, CPT> hr[TPT];
     Raw<DT, CPT> dr[LMAX];
 #pragma unroll
-    for (int k = 0; k < kK; ++k) load_at<DT, CPT, true>(high, ho + (k / kS) * row_b + (k % kS) * tap_b, hr[k]);
+    for (int k = 0; k < TPT; ++k) load_at<DT, CPT, true>(high, ho + (k / kS) * row_b + (k % kS) * tap_b, hr[k]);
 #pragma unroll
     for (int l = 0; l < LMAX; ++l) load_at<DT, CPT>(low.p[l < L ? l : 0], zo, dr[l]);
     LTHC_PHASE_BARRIER();
-    float h[kK][CPT];
+    float h[TPT][CPT];
 #pragma unroll
-    for (int k = 0; k < kK; ++k) unpack_raw<DT, CPT>(hr[k], h[k]);
+    for (int k = 0; k < TPT; ++k) unpack_raw<DT, CPT>(hr[k], h[k]);
 #pragma unroll
     for (int l = 0; l < LMAX; ++l) {
       float d[CPT];
@@ -732,7 +750,7 @@ __global__ __launch_bounds__(kBlock) void cell_wgrad_kernel(const void* __restri
 #pragma unroll
       for (int v = 0; v < CPT; ++v)
 #pragma unroll
-        for (int k = 0; k < kK; ++k) acc[l][v][k] = fmaf(h[k][v], d[v], acc[l][v][k]);
+        for (int k = 0; k < TPT; ++k) acc[l][v][k] = fmaf(h[k][v], d[v], acc[l][v][k]);
     }
   }
   float* dst = partial + static_cast<int64_t>(blockIdx.x) * L * C * kK;
@@ -741,9 +759,9 @@ __global__ __launch_bounds__(kBlock) void cell_wgrad_kernel(const void* __restri
     if (l < L) {
 #pragma unroll
       for (int v = 0; v < CPT; ++v) {
-        float4* row = reinterpret_cast<float4*>(dst + (static_cast<int64_t>(l) * C + c0 + v) * kK);
+        float4* row = reinterpret_cast<float4*>(dst + (static_cast<int64_t>(l) * C + c0 + v) * kK + tap0);
 #pragma unroll
-        for (int q = 0; q < 4; ++q)
+        for (int q = 0; q < TPT / 4; ++q)
           row[q] = make_float4(acc[l][v][4 * q], acc[l][v][4 * q + 1], acc[l][v][4 * q + 2], acc[l][v][4 * q + 3]);
       }
     }
@@ -989,13 +1007,19 @@ int64_t grid_step_cells(int64_t want, int64_t ncells, int G, int cpi) {
   return std::max<int64_t>(unit, std::min<int64_t>(want / unit * unit, cap));
 }
 
-// Channels per thread of the whole-cell kernels per depth bucket: the
-// LMAX x CPT x 16 fp32 weights, one cell's loads and the 16 x CPT
-// accumulators fit in 256 VGPRs.
+// Shape of the whole-cell kernels per depth bucket: channels per thread CPT
+// and groups per block GR (tap groups of the materialise / weight gradient,
+// layer groups of the multi-weight read).  The LMAX x CPT x 16 / GR fp32
+// weights (or accumulators), one cell's loads and the accumulators fit in
+// 256 VGPRs: one group up to depth 12, two up to depth 24.
 template <int DT, int LMAX>
 struct CellMatShape {
   static constexpr int CPT = DT == LTHC_F32 ? (LMAX <= 1 ? 2 : 1) : (LMAX <= 1 ? 4 : (LMAX <= 4 ? 2 : 1));
+  static constexpr int GR = LMAX <= 12 ? 1 : 2;
 };
+
+// Depth buckets of the whole-cell kernels.
+constexpr int kCellMaxDepth = 24;
 
 // Blocks of `kernel` (kBlock threads) resident on one CU.
 template <typename K>
@@ -1081,15 +1105,15 @@ void wgrad_shape(int L, int& tpt, int& cpt);
 
 template <int DT, int LMAX>
 void cell_wgrad_plan_l(WgradPlan& p, int64_t ncells, int G, int64_t C) {
-  constexpr int CPT = CellMatShape<DT, LMAX>::CPT;
-  static const int per_cu = resident_blocks(cell_wgrad_kernel<DT, LMAX, CPT>);
-  p.slabs = static_cast<int>((C / CPT + kBlock - 1) / kBlock);
+  constexpr int CPT = CellMatShape<DT, LMAX>::CPT, GR = CellMatShape<DT, LMAX>::GR;
+  static const int per_cu = resident_blocks(cell_wgrad_kernel<DT, LMAX, CPT, GR>);
+  p.slabs = static_cast<int>((C / CPT + kBlock / GR - 1) / (kBlock / GR));
   p.nbx = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu / p.slabs, ncells, G, 1);
 }
 
 WgradPlan wgrad_plan(int dt, int64_t ncells, int G, int64_t C, int L, int blocks_per_cu = 2) {
   WgradPlan p{};
-  if (ncells > 0 && L <= 12 && fits32(ncells * kK * C * esize(dt))) {
+  if (ncells > 0 && L <= kCellMaxDepth && fits32(ncells * kK * C * esize(dt))) {
     p.cell = true;
     dispatch_dtype(dt, [&](auto d) {
       constexpr int DT = decltype(d)::value;
@@ -1097,7 +1121,9 @@ WgradPlan wgrad_plan(int dt, int64_t ncells, int G, int64_t C, int L, int blocks
       else if (L <= 2) cell_wgrad_plan_l<DT, 2>(p, ncells, G, C);
       else if (L <= 4) cell_wgrad_plan_l<DT, 4>(p, ncells, G, C);
       else if (L <= 8) cell_wgrad_plan_l<DT, 8>(p, ncells, G, C);
-      else cell_wgrad_plan_l<DT, 12>(p, ncells, G, C);
+      else if (L <= 12) cell_wgrad_plan_l<DT, 12>(p, ncells, G, C);
+      else if (L <= 16) cell_wgrad_plan_l<DT, 16>(p, ncells, G, C);
+      else cell_wgrad_plan_l<DT, 24>(p, ncells, G, C);
     });
     return p;
   }
@@ -1187,10 +1213,10 @@ void launch_mat_l(const void* base, const PtrPack& dz, const PtrPack& beta, void
 template <int DT, int WDT, int LMAX, bool HAS_BASE, bool EXACT>
 void launch_cell_mat(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells, int G,
                      int C, hipStream_t st) {
-  constexpr int CPT = CellMatShape<DT, LMAX>::CPT;
-  const auto kernel = cell_mat_kernel<DT, WDT, LMAX, CPT, HAS_BASE, EXACT>;
+  constexpr int CPT = CellMatShape<DT, LMAX>::CPT, GR = CellMatShape<DT, LMAX>::GR;
+  const auto kernel = cell_mat_kernel<DT, WDT, LMAX, CPT, GR, HAS_BASE, EXACT>;
   static const int per_cu = resident_blocks(kernel);
-  const int slabs = (C / CPT + kBlock - 1) / kBlock;
+  const int slabs = (C / CPT + kBlock / GR - 1) / (kBlock / GR);
   const int64_t per = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu / slabs, ncells, G, 1);
   kernel<<<dim3(static_cast<unsigned>(per), slabs), kBlock, 0, st>>>(base, dz, beta, out, L,
                                                                     static_cast<uint32_t>(ncells), G, C);
@@ -1215,12 +1241,14 @@ void launch_materialise(const void* base, const PtrPack& dz, const PtrPack& beta
     }
     return;
   }
-  if (off32 && L <= 12) {  // whole-cell kernel: weights of every tap in VGPRs
+  if (off32 && L <= kCellMaxDepth) {  // whole-cell kernel: weights of every tap in VGPRs
     if (L <= 1) launch_cell_mat_l<DT, WDT, 1>(base, dz, beta, out, L, ncells, G, C, st);
     else if (L <= 2) launch_cell_mat_l<DT, WDT, 2>(base, dz, beta, out, L, ncells, G, C, st);
     else if (L <= 4) launch_cell_mat_l<DT, WDT, 4>(base, dz, beta, out, L, ncells, G, C, st);
     else if (L <= 8) launch_cell_mat_l<DT, WDT, 8>(base, dz, beta, out, L, ncells, G, C, st);
-    else launch_cell_mat_l<DT, WDT, 12>(base, dz, beta, out, L, ncells, G, C, st);
+    else if (L <= 12) launch_cell_mat_l<DT, WDT, 12>(base, dz, beta, out, L, ncells, G, C, st);
+    else if (L <= 16) launch_cell_mat_l<DT, WDT, 16>(base, dz, beta, out, L, ncells, G, C, st);
+    else launch_cell_mat_l<DT, WDT, 24>(base, dz, beta, out, L, ncells, G, C, st);
     return;
   }
   if (L <= 1) launch_mat_l<DT, WDT, 1>(base, dz, beta, out, L, ncells, G, C, off32, st);
@@ -1244,8 +1272,8 @@ void launch_wgrad_t(const void* high, const PtrPack& low, float* partial, int L,
 template <int DT, int LMAX>
 void launch_cell_wgrad(const void* high, const PtrPack& low, float* partial, int L, int64_t ncells, int G, int C,
                        const WgradPlan& p, hipStream_t st) {
-  constexpr int CPT = CellMatShape<DT, LMAX>::CPT;
-  cell_wgrad_kernel<DT, LMAX, CPT><<<dim3(static_cast<unsigned>(p.nbx), p.slabs), kBlock, 0, st>>>(
+  constexpr int CPT = CellMatShape<DT, LMAX>::CPT, GR = CellMatShape<DT, LMAX>::GR;
+  cell_wgrad_kernel<DT, LMAX, CPT, GR><<<dim3(static_cast<unsigned>(p.nbx), p.slabs), kBlock, 0, st>>>(
       high, low, partial, L, static_cast<uint32_t>(ncells), G, C);
 }
 
@@ -1258,7 +1286,9 @@ void launch_wgrad(const void* high, const PtrPack& low, float* partial, int L, i
       else if (L <= 2) launch_cell_wgrad<DT, 2>(high, low, partial, L, ncells, G, C, p, st);
       else if (L <= 4) launch_cell_wgrad<DT, 4>(high, low, partial, L, ncells, G, C, p, st);
       else if (L <= 8) launch_cell_wgrad<DT, 8>(high, low, partial, L, ncells, G, C, p, st);
-      else launch_cell_wgrad<DT, 12>(high, low, partial, L, ncells, G, C, p, st);
+      else if (L <= 12) launch_cell_wgrad<DT, 12>(high, low, partial, L, ncells, G, C, p, st);
+      else if (L <= 16) launch_cell_wgrad<DT, 16>(high, low, partial, L, ncells, G, C, p, st);
+      else launch_cell_wgrad<DT, 24>(high, low, partial, L, ncells, G, C, p, st);
       return;
     }
   }
@@ -1290,10 +1320,10 @@ void launch_read_multi_t(const void* g, const PtrPack& w, const PtrPack& out, in
 template <int DT, int WDT, int LMAX>
 void launch_cell_read_multi(const void* g, const PtrPack& w, const PtrPack& out, int L, int64_t ncells, int G, int C,
                             hipStream_t st) {
-  constexpr int CPT = CellMatShape<DT, LMAX>::CPT;
-  const auto kernel = cell_read_multi_kernel<DT, WDT, LMAX, CPT>;
+  constexpr int CPT = CellMatShape<DT, LMAX>::CPT, GR = CellMatShape<DT, LMAX>::GR;
+  const auto kernel = cell_read_multi_kernel<DT, WDT, LMAX, CPT, GR>;
   static const int per_cu = resident_blocks(kernel);
-  const int slabs = (C / CPT + kBlock - 1) / kBlock;
+  const int slabs = (C / CPT + kBlock / GR - 1) / (kBlock / GR);
   const int64_t per = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu / slabs, ncells, G, 1);
   kernel<<<dim3(static_cast<unsigned>(per), slabs), kBlock, 0, st>>>(g, w, out, L, static_cast<uint32_t>(ncells), G, C);
 }
@@ -1302,12 +1332,14 @@ template <int DT, int WDT, typename Off>
 void launch_read_multi(const void* g, const PtrPack& w, const PtrPack& out, int L, int64_t ncells, int G, int C,
                        hipStream_t st) {
   if constexpr (std::is_same_v<Off, uint32_t>) {  // whole-cell kernel: every layer's weights in VGPRs
-    if (L <= 12) {
+    if (L <= kCellMaxDepth) {
       if (L <= 1) launch_cell_read_multi<DT, WDT, 1>(g, w, out, L, ncells, G, C, st);
       else if (L <= 2) launch_cell_read_multi<DT, WDT, 2>(g, w, out, L, ncells, G, C, st);
       else if (L <= 4) launch_cell_read_multi<DT, WDT, 4>(g, w, out, L, ncells, G, C, st);
       else if (L <= 8) launch_cell_read_multi<DT, WDT, 8>(g, w, out, L, ncells, G, C, st);
-      else launch_cell_read_multi<DT, WDT, 12>(g, w, out, L, ncells, G, C, st);
+      else if (L <= 12) launch_cell_read_multi<DT, WDT, 12>(g, w, out, L, ncells, G, C, st);
+      else if (L <= 16) launch_cell_read_multi<DT, WDT, 16>(g, w, out, L, ncells, G, C, st);
+      else launch_cell_read_multi<DT, WDT, 24>(g, w, out, L, ncells, G, C, st);
       return;
     }
   }
