@@ -217,19 +217,19 @@ def interface_forward(args, torch, dev, ops, B, G, C, L):
     for _ in range(2):
         x0 = torch.randn((B, H, H, C), generator=gen, device=dev).to(bf16)
         dzs = [(torch.randn((B, G * G, C), generator=gen, device=dev) * 0.02).to(bf16) for _ in range(L)]
-        sets.append((x0, dzs, torch.stack(dzs) if L != 12 else None))
+        sets.append((x0, dzs))
     stream = torch.cuda.current_stream()
 
     def step(i):
-        x0, dzs, stack = sets[i % 2]
+        x0, dzs = sets[i % 2]
         z = ops.local_write_traceable(x0, alpha)
         gam = ops.lazy_gamma_stack(alpha, beta_stack)
         for l in range(L):
             z = ops.lazy_workspace_update(z, dzs[l], gam[l])
         if L == 12:
             xl = ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas)
-        else:  # the dZ stack is an input here, as the transformer would write it
-            xl = ops.final_accumulate_b4_traceable(x0, stack, beta_stack)
+        else:
+            xl = ops.final_accumulate_list(x0, dzs, betas)
         return z, xl
 
     side = torch.cuda.Stream()
@@ -297,8 +297,8 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
             dzv.append(d)
         if L == 12:
             xl = ops.final_accumulate_b4_12_traceable(x0v, *dzv, *betas)
-        else:  # the base-class materialisation (stacked op)
-            xl = ops.final_accumulate_b4_traceable(x0v, torch.stack(dzv), torch.stack(betas))
+        else:  # the base-class materialisation of the model (list op)
+            xl = ops.final_accumulate_list(x0v, dzv, betas)
         return xl, zs[:L]
 
     leaves = [x0, alpha] + betas + dzs

@@ -419,11 +419,12 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
 
     # -- interface ---------------------------------------------------------------------------------
     def final_accumulate_reference(self, x0: torch.Tensor, dz_list: list[torch.Tensor]) -> torch.Tensor:
-        """X_L = X0 + sum_l P_l(dZ_l) in one pass (the reference's generic loop, local_thc.py:1368-1372)."""
+        """X_L = X0 + sum_l P_l(dZ_l) in one pass (the reference's generic loop, local_thc.py:1368-1372), the
+        layers passed as lists so no dZ stack is built."""
         if len(dz_list) != len(self.blocks):
             raise ValueError(f"expected {len(self.blocks)} updates, got {len(dz_list)}")
-        betas = torch.stack([blk.write.channel_beta(dtype=torch.float32) for blk in self.blocks])
-        return ops.final_accumulate_b4_traceable(x0, torch.stack(dz_list), betas)
+        betas = [blk.write.channel_beta(dtype=torch.float32) for blk in self.blocks]
+        return ops.final_accumulate_list(x0, list(dz_list), betas)
 
     def _conditioning(self, t: torch.Tensor, y: torch.Tensor):
         c = self.t_embedder(t) + self.y_embedder(y)

@@ -434,6 +434,106 @@ torch.library.register_autograd(
 
 
 # ---------------------------------------------------------------------------
+# MATERIALISE, any depth as a list of layers (no reference op: the reference's
+# generic path is the Python write_add loop of local_thc.py:1368-1372, and its
+# stacked op is fixed to the 64x64 / 16x16 geometry)
+# ---------------------------------------------------------------------------
+def _check_list(x0: Tensor, dzs: Sequence[Tensor], betas: Sequence[Tensor]) -> int:
+    b, g, c = _hi_geom(x0, "x0")
+    L = len(dzs)
+    if L != len(betas) or not 1 <= L <= _abi.MAX_LAYERS:
+        raise ValueError(f"expected 1..{_abi.MAX_LAYERS} dz and as many beta tensors, got {len(dzs)} and {len(betas)}")
+    for i, (dz, bt) in enumerate(zip(dzs, betas)):
+        if tuple(dz.shape) != (b, g * g, c):
+            raise ValueError(f"dz[{i}] must be [{b},{g * g},{c}], got {tuple(dz.shape)}")
+        _check_weight(bt, c, f"beta[{i}]")
+    return L
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_list", mutates_args=())
+def final_accumulate_list(x0: Tensor, dzs: list[Tensor], betas: list[Tensor]) -> Tensor:
+    """X_L = x0 + sum_l betas[l][c,k] dzs[l][b,m,c] in x0.dtype, one pass, the L layers passed as lists."""
+    _on_gpu(x0, *dzs, *betas)
+    _check_list(x0, dzs, betas)
+    x0 = _prep(x0)
+    dzs = _same_dtype(x0, [_prep(d) for d in dzs])
+    betas = [_prep_w(bt, x0.dtype) for bt in betas]
+    if len({bt.dtype for bt in betas}) != 1:
+        betas = [bt.float() for bt in betas]
+    out = torch.empty_like(x0)
+    _launch_materialise(x0, dzs, betas, out)
+    return out
+
+
+@final_accumulate_list.register_fake
+def _(x0: Tensor, dzs: list[Tensor], betas: list[Tensor]) -> Tensor:
+    return torch.empty_like(x0)
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_list_grad_dz", mutates_args=())
+def final_accumulate_list_grad_dz(grad_out: Tensor, betas: list[Tensor]) -> list[Tensor]:
+    """gdZ_l[b,m,c] = sum_k betas[l][c,k] grad_out[b,m,k,c], one tensor per layer, in grad_out.dtype."""
+    _on_gpu(grad_out, *betas)
+    b, g, c = _hi_geom(grad_out, "grad_out")
+    for i, bt in enumerate(betas):
+        _check_weight(bt, c, f"beta[{i}]")
+    grad_out = _prep(grad_out)
+    betas = [_prep_w(bt, grad_out.dtype) for bt in betas]
+    if len({bt.dtype for bt in betas}) != 1:
+        betas = [bt.float() for bt in betas]
+    outs = [torch.empty((b, g * g, c), device=grad_out.device, dtype=grad_out.dtype) for _ in betas]
+    _launch_read_multi(grad_out, betas, outs)
+    return outs
+
+
+@final_accumulate_list_grad_dz.register_fake
+def _(grad_out: Tensor, betas: list[Tensor]) -> list[Tensor]:
+    b, g, c = _hi_geom(grad_out, "grad_out")
+    return [grad_out.new_empty((b, g * g, c)) for _ in betas]
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_list_grad_beta", mutates_args=())
+def final_accumulate_list_grad_beta(grad_out: Tensor, dzs: list[Tensor]) -> Tensor:
+    """gbeta[l,c,k] = sum_{b,m} grad_out[b,m,k,c] dzs[l][b,m,c] in fp32 [L,C,16] (deterministic order)."""
+    _on_gpu(grad_out, *dzs)
+    b, g, c = _hi_geom(grad_out, "grad_out")
+    for i, dz in enumerate(dzs):
+        if tuple(dz.shape) != (b, g * g, c):
+            raise ValueError(f"dz[{i}] must be [{b},{g * g},{c}], got {tuple(dz.shape)}")
+    grad_out = _prep(grad_out)
+    dzs = _same_dtype(grad_out, [_prep(d) for d in dzs])
+    return _launch_weight_grad(grad_out, dzs)
+
+
+@final_accumulate_list_grad_beta.register_fake
+def _(grad_out: Tensor, dzs: list[Tensor]) -> Tensor:
+    return grad_out.new_empty((len(dzs), grad_out.shape[3], K), dtype=torch.float32)
+
+
+def _setup_final_accumulate_list_ctx(ctx, inputs, output):
+    _, dzs, betas = inputs
+    ctx.save_for_backward(*dzs, *betas)
+    ctx.L = len(dzs)
+
+
+def _backward_final_accumulate_list(ctx, grad_out):
+    saved = ctx.saved_tensors
+    dzs, betas = saved[: ctx.L], saved[ctx.L :]
+    grad_out = grad_out.contiguous()
+    grad_dzs = final_accumulate_list_grad_dz(grad_out, list(betas)) if ctx.needs_input_grad[1] else None
+    grad_betas = None
+    if ctx.needs_input_grad[2]:
+        gb = final_accumulate_list_grad_beta(grad_out, list(dzs))
+        grad_betas = [g.to(dtype=bt.dtype) for g, bt in zip(gb.unbind(0), betas, strict=True)]
+    return grad_out, grad_dzs, grad_betas
+
+
+torch.library.register_autograd(
+    final_accumulate_list, _backward_final_accumulate_list, setup_context=_setup_final_accumulate_list_ctx
+)
+
+
+# ---------------------------------------------------------------------------
 # MATERIALISE, 12 separate layers (jit_thc::final_accumulate_b4_12_traceable,
 # local_thc_triton_kernels.py:1669-1736) and its backward ops (:1800-1919)
 # ---------------------------------------------------------------------------

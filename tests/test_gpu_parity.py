@@ -229,6 +229,27 @@ def test_config5_shape_bf16(coracle):
     assert_f32(host(capi.weight_grad(g, dzs)), coracle.Cweight_grad(gh, dzh, G), what="gbeta")
 
 
+def test_config5_list_op_and_autograd_bf16(coracle):
+    """jit_thc::final_accumulate_list at configuration 5's shape: forward, and its autograd (gdZ_l, gbeta_l)."""
+    B, G, C, L = 2, 32, 1024, 24
+    d = cfg(B, G, C, L, seed=4, grads=True)
+    x0 = dev(d["x0"], BF16).requires_grad_(True)
+    betas = [dev(b).requires_grad_(True) for b in d["beta"]]
+    dzs = [dev(z, BF16).requires_grad_(True) for z in d["dz"]]
+    xl = ops.final_accumulate_list(x0, dzs, betas)
+    x0h, dzh = host(x0), [host(z) for z in dzs]
+    assert_bf16(host(xl), coracle.Cwrite(x0h, dzh, list(d["beta"])), what="X_L")
+    g = dev(d["grad_xl"], BF16)
+    xl.backward(g)
+    assert torch.equal(x0.grad, g)
+    gh = host(g)
+    ref_dz = coracle.Cread_multi(gh, list(d["beta"]), G)
+    ref_beta = coracle.Cweight_grad(gh, dzh, G)
+    for l in range(L):
+        assert_bf16(host(dzs[l].grad), ref_dz[l], what=f"gdZ_{l}")
+        assert_f32(host(betas[l].grad), ref_beta[l], tol=1e-5, what=f"gbeta_{l}")
+
+
 # ---------------------------------------------------------------------------
 # edge cases: ragged channel counts, every depth bucket, batch 1 and 0
 # ---------------------------------------------------------------------------
