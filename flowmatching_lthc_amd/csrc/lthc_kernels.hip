@@ -1593,3 +1593,6 @@ int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dty
 }
 
 }  // extern "C"
+
+// Final-layer RMSNorm + modulate of the decoder input (the materialisation's consumer).
+#include "norm_modulate.inc"

@@ -105,7 +105,10 @@ class BottleneckPatchEmbedNHWC(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if tuple(x.shape[-2:]) != self.img_size:
             raise ValueError(f"expected image size {self.img_size}, got {tuple(x.shape[-2:])}")
-        return self.proj2(self.proj1(x)).permute(0, 2, 3, 1).contiguous()
+        # proj2 is a 1x1 convolution: as a linear map over the channels of proj1's output viewed NHWC it writes
+        # the NHWC residual directly (no permute copy of the C-channel tensor)
+        h = self.proj1(x).permute(0, 2, 3, 1)
+        return F.linear(h, self.proj2.weight.view(self.proj2.out_channels, -1), self.proj2.bias)
 
 
 class TimestepEmbedder(nn.Module):
@@ -244,6 +247,10 @@ class FinalLayerSharedAdaLN(nn.Module):
 
     def forward(self, x: torch.Tensor, t2: torch.Tensor) -> torch.Tensor:
         shift, scale = t2.chunk(2, dim=1)
+        if x.is_cuda and shift.dtype == x.dtype and x.shape[-1] % 4 == 0 and x.shape[-1] <= 2048:
+            # one HIP pass: RMSNorm + modulate with the eager op sequence's roundings (jit_thc::norm_modulate)
+            y, _ = ops.norm_modulate(x, self.norm_final.weight, shift.contiguous(), scale.contiguous(), self.norm_final.eps)
+            return self.linear(y)
         return self.linear(modulate(self.norm_final(x), shift, scale))
 
 

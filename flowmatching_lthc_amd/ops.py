@@ -826,6 +826,98 @@ def _backward_gamma(ctx, grad):
 torch.library.register_autograd(lazy_gamma_stack, _backward_gamma, setup_context=_setup_gamma_ctx)
 
 
+# ---------------------------------------------------------------------------
+# FINAL-LAYER RMSNORM + MODULATE (no reference op: FinalLayerSharedAdaLN's
+# norm_final + modulate, local_thc.py:870-873, is eager torch)
+# ---------------------------------------------------------------------------
+def _check_norm(x: Tensor, weight: Tensor, shift: Tensor, scale: Tensor) -> tuple[int, int, int]:
+    if x.dim() != 3:
+        raise ValueError(f"x must be [B,N,C], got {tuple(x.shape)}")
+    b, n, c = x.shape
+    if tuple(weight.shape) != (c,) or tuple(shift.shape) != (b, c) or tuple(scale.shape) != (b, c):
+        raise ValueError(
+            f"weight [{c}], shift and scale [{b},{c}] expected, got {tuple(weight.shape)}, "
+            f"{tuple(shift.shape)}, {tuple(scale.shape)}"
+        )
+    if shift.dtype != x.dtype or scale.dtype != x.dtype:
+        raise ValueError(f"shift and scale must have x's dtype {x.dtype}, got {shift.dtype}, {scale.dtype}")
+    if c % 4 != 0 or c > 2048:
+        raise ValueError(f"channels {c} must be a multiple of 4 and at most 2048")
+    _abi.code(x)
+    return b, n, c
+
+
+@torch.library.custom_op("jit_thc::norm_modulate", mutates_args=())
+def norm_modulate(x: Tensor, weight: Tensor, shift: Tensor, scale: Tensor, eps: float) -> tuple[Tensor, Tensor]:
+    """(modulate(RMSNorm(x), shift, scale) in x.dtype, fp32 [B*N] inverse RMS) in one pass over x."""
+    _on_gpu(x, weight, shift, scale)
+    b, n, c = _check_norm(x, weight, shift, scale)
+    x, shift, scale = _prep(x), _prep(shift), _prep(scale)
+    w = weight.float().contiguous()
+    y = torch.empty_like(x)
+    inv = torch.empty((b * n,), device=x.device, dtype=torch.float32)
+    with _on_device(x):
+        rc = _abi.load().lthc_norm_modulate_fwd(
+            x.data_ptr(), _abi.code(x), w.data_ptr(), shift.data_ptr(), scale.data_ptr(), y.data_ptr(),
+            inv.data_ptr(), b, n, c, eps, _abi.stream_of(x),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_norm_modulate_fwd")
+    return y, inv
+
+
+@norm_modulate.register_fake
+def _(x: Tensor, weight: Tensor, shift: Tensor, scale: Tensor, eps: float):
+    return torch.empty_like(x), x.new_empty((x.shape[0] * x.shape[1],), dtype=torch.float32)
+
+
+@torch.library.custom_op("jit_thc::norm_modulate_backward", mutates_args=())
+def norm_modulate_backward(
+    grad: Tensor, x: Tensor, weight: Tensor, scale: Tensor, inv: Tensor
+) -> tuple[Tensor, Tensor, Tensor, Tensor]:
+    """(dx in x.dtype, dweight fp32 [C], dshift fp32 [B,C], dscale fp32 [B,C])."""
+    _on_gpu(grad, x, weight, scale, inv)
+    b, n, c = _check_norm(x, weight, scale, scale)
+    (grad,) = _same_dtype(x, [_prep(grad)])
+    x, scale, inv = _prep(x), _prep(scale), inv.float().contiguous()
+    w = weight.float().contiguous()
+    gx = torch.empty_like(x)
+    gw = torch.empty((c,), device=x.device, dtype=torch.float32)
+    gsh = torch.empty((b, c), device=x.device, dtype=torch.float32)
+    gsc = torch.empty((b, c), device=x.device, dtype=torch.float32)
+    ws = torch.empty((max(_abi.norm_modulate_bwd_workspace_bytes(b, n, c), 16),), device=x.device, dtype=torch.uint8)
+    with _on_device(x):
+        rc = _abi.load().lthc_norm_modulate_bwd(
+            grad.data_ptr(), x.data_ptr(), _abi.code(x), w.data_ptr(), scale.data_ptr(), inv.data_ptr(),
+            gx.data_ptr(), gw.data_ptr(), gsh.data_ptr(), gsc.data_ptr(), b, n, c, ws.data_ptr(), ws.numel(),
+            _abi.stream_of(x),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_norm_modulate_bwd")
+    return gx, gw, gsh, gsc
+
+
+@norm_modulate_backward.register_fake
+def _(grad: Tensor, x: Tensor, weight: Tensor, scale: Tensor, inv: Tensor):
+    b, n, c = x.shape
+    f32 = torch.float32
+    return torch.empty_like(x), x.new_empty((c,), dtype=f32), x.new_empty((b, c), dtype=f32), x.new_empty((b, c), dtype=f32)
+
+
+def _setup_norm_ctx(ctx, inputs, output):
+    x, weight, shift, scale, _ = inputs
+    ctx.save_for_backward(x, weight, scale, output[1])
+    ctx.dtypes = (weight.dtype, shift.dtype, scale.dtype)
+
+
+def _backward_norm(ctx, grad_y, grad_inv):
+    x, weight, scale, inv = ctx.saved_tensors
+    gx, gw, gsh, gsc = norm_modulate_backward(grad_y.contiguous(), x, weight, scale, inv)
+    wd, shd, scd = ctx.dtypes
+    return gx, gw.to(wd), gsh.to(shd), gsc.to(scd), None
+
+
+torch.library.register_autograd(norm_modulate, _backward_norm, setup_context=_setup_norm_ctx)
+
+
 # Reference-style aliases (local_thc_triton_kernels.py exports these names).
 triton_final_accumulate_b4_traceable = final_accumulate_b4_traceable
 triton_final_accumulate_b4_12_traceable = final_accumulate_b4_12_traceable

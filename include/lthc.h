@@ -157,6 +157,31 @@ int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dty
                    int g_dtype, void* gdz, float* ggamma, int64_t rows, int64_t C,
                    void* workspace, size_t workspace_bytes, void* stream);
 
+/*
+ * FINAL-LAYER RMSNORM + ADALN MODULATE (the consumer of the materialisation)
+ *   inv[t]  = rsqrt(mean_c x[t,c]^2 + eps)                           fp32 [B*N] (may be NULL)
+ *   y[t,c]  = r(r(r((x*inv)*weight[c]) * r(1 + scale[b,c])) + shift[b,c])
+ * for token t = b*N + n of x [B, N, C], r = round to x_dtype (identity for
+ * fp32).  shift and scale are [B, C] in x_dtype; weight is fp32 [C].
+ * Replaces FinalLayerSharedAdaLN's norm_final + modulate
+ * (local_thc.py:870-873, RMSNorm jit_shared_adaln.py:26-30, modulate
+ * local_thc.py:37-38), which eager PyTorch evaluates as about eight passes
+ * over the [B, N, C] tensor; here one read and one write.  C <= 2048.
+ */
+int lthc_norm_modulate_fwd(const void* x, int x_dtype, const float* weight, const void* shift, const void* scale,
+                           void* y, float* inv, int64_t B, int64_t N, int64_t C, float eps, void* stream);
+
+/*
+ * Its backward, given gy = dL/dy and the forward's inv:
+ *   gx (x_dtype), gweight fp32 [C], gshift fp32 [B,C], gscale fp32 [B,C]
+ * (the fp32 gradient of the function above; reductions in a fixed order).
+ */
+size_t lthc_norm_modulate_bwd_workspace_bytes(int64_t B, int64_t N, int64_t C);
+int lthc_norm_modulate_bwd(const void* gy, const void* x, int x_dtype, const float* weight, const void* scale,
+                           const float* inv, void* gx, float* gweight, float* gshift, float* gscale,
+                           int64_t B, int64_t N, int64_t C, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -368,3 +368,57 @@ def test_hip_graph_replay_matches_eager():
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {i}"
         assert torch.equal(gb, gb_eager), f"replay {i}"
+
+
+# ---------------------------------------------------------------------------
+# final-layer RMSNorm + modulate (jit_thc::norm_modulate, the materialisation's consumer)
+# ---------------------------------------------------------------------------
+def _eager_norm_modulate(x, w, shift, scale, eps=1e-6):
+    """The reference's op sequence (jit_shared_adaln.py:26-30, local_thc.py:37-38) in torch."""
+    xf = x.float()
+    xf = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    n = (xf * w).to(x.dtype)
+    return n * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1)
+
+
+@pytest.mark.parametrize("dtype,C", [(F32, 768), (BF16, 768), (BF16, 1024), (F32, 260)])
+def test_norm_modulate_forward_and_backward(dtype, C):
+    g = torch.Generator().manual_seed(11)
+    B, N = 3, 257
+    x64 = torch.randn(B, N, C, generator=g, dtype=torch.float64)
+    w64 = 1 + 0.1 * torch.randn(C, generator=g, dtype=torch.float64)
+    sh64 = 0.2 * torch.randn(B, C, generator=g, dtype=torch.float64)
+    sc64 = 0.2 * torch.randn(B, C, generator=g, dtype=torch.float64)
+    gy64 = torch.randn(B, N, C, generator=g, dtype=torch.float64)
+    x, sh, sc, gy = (t.to(DEV, dtype) for t in (x64, sh64, sc64, gy64))
+    w = w64.to(DEV, F32)
+    y, inv = ops.norm_modulate(x, w, sh, sc, 1e-6)
+    ref_eager = _eager_norm_modulate(x, w, sh, sc)
+    # exact function on the same (rounded) inputs in fp64, without intermediate roundings
+    xd, wd, shd, scd = (t.double().cpu() for t in (x, w, sh, sc))
+    inv64 = torch.rsqrt(xd.pow(2).mean(-1, keepdim=True) + 1e-6)
+    exact = (xd * inv64 * wd) * (1 + scd.unsqueeze(1)) + shd.unsqueeze(1)
+    assert_f32(host(inv), inv64.reshape(-1).numpy(), tol=1e-6, what="inv")
+    if dtype == F32:
+        assert_f32(host(y), exact.numpy(), tol=1e-5, what="y fp32")
+    else:  # no further from the exact function than the eager bf16 sequence itself
+        err = (y.double().cpu() - exact).abs().max().item()
+        err_eager = (ref_eager.double().cpu() - exact).abs().max().item()
+        assert err <= 1.5 * err_eager + 1e-6, (err, err_eager)
+    # backward against torch autograd of the fp64 function
+    xr, wr, shr, scr = (t.double().cpu().requires_grad_(True) for t in (x, w, sh, sc))
+    inv_r = torch.rsqrt(xr.pow(2).mean(-1, keepdim=True) + 1e-6)
+    yr = (xr * inv_r * wr) * (1 + scr.unsqueeze(1)) + shr.unsqueeze(1)
+    yr.backward(gy.double().cpu())
+    gx, gw, gsh, gsc = ops.norm_modulate_backward(gy, x, w, sc, inv)
+    tol = 1e-5 if dtype == F32 else 1e-2
+    assert_f32(host(gx), xr.grad.numpy(), tol=tol, what="dx")
+    assert_f32(host(gw), wr.grad.numpy(), tol=max(tol, 1e-4), what="dweight")
+    assert_f32(host(gsh), shr.grad.numpy(), tol=1e-5, what="dshift")
+    assert_f32(host(gsc), scr.grad.numpy(), tol=max(tol, 1e-4), what="dscale")
+    # the autograd registration returns the same gradients
+    xa, wa, sha, sca = (t.clone().requires_grad_(True) for t in (x, w, sh, sc))
+    ya, _ = ops.norm_modulate(xa, wa, sha, sca, 1e-6)
+    ya.backward(gy)
+    assert torch.equal(xa.grad, gx) and torch.equal(wa.grad, gw.to(wa.dtype))
+    assert torch.equal(sha.grad, gsh.to(dtype)) and torch.equal(sca.grad, gsc.to(dtype))
