@@ -47,6 +47,18 @@ class RMSNorm(nn.Module):
         return (xf * inv * self.weight).to(x.dtype)
 
 
+def norm_modulate(norm: RMSNorm, x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
+    """modulate(norm(x), shift, scale) for x [B, N, C] and per-sample [B, C] shift / scale.
+
+    On the GPU, when shift and scale share x's dtype (bf16 autocast or fp32), one HIP pass with the eager
+    sequence's roundings (jit_thc::norm_modulate); otherwise the eager sequence itself (other dtype mixes
+    follow torch's promotion rules, which the kernel does not implement).
+    """
+    if x.is_cuda and x.dim() == 3 and shift.dtype == x.dtype and scale.dtype == x.dtype and x.shape[-1] % 4 == 0 and x.shape[-1] <= 2048:
+        return ops.norm_modulate(x, norm.weight, shift.contiguous(), scale.contiguous(), norm.eps)[0]
+    return modulate(norm(x), shift, scale)
+
+
 def _rotate_pairs(x: torch.Tensor) -> torch.Tensor:
     """(x0, x1, x2, x3, ...) -> (-x1, x0, -x3, x2, ...): rotation of interleaved pairs."""
     pairs = x.unflatten(-1, (-1, 2))
@@ -232,8 +244,8 @@ class WorkspaceSharedAdaLNBranch(nn.Module):
 
     def forward(self, z: torch.Tensor, t6: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> torch.Tensor:
         sh_a, sc_a, g_a, sh_m, sc_m, g_m = t6.chunk(6, dim=-1)
-        d_attn = g_a.unsqueeze(1) * self.attn(modulate(self.norm1(z), sh_a, sc_a), rope)
-        d_mlp = g_m.unsqueeze(1) * self.mlp(modulate(self.norm2(z + d_attn), sh_m, sc_m))
+        d_attn = g_a.unsqueeze(1) * self.attn(norm_modulate(self.norm1, z, sh_a, sc_a), rope)
+        d_mlp = g_m.unsqueeze(1) * self.mlp(norm_modulate(self.norm2, z + d_attn, sh_m, sc_m))
         return d_attn + d_mlp
 
 
@@ -247,11 +259,7 @@ class FinalLayerSharedAdaLN(nn.Module):
 
     def forward(self, x: torch.Tensor, t2: torch.Tensor) -> torch.Tensor:
         shift, scale = t2.chunk(2, dim=1)
-        if x.is_cuda and shift.dtype == x.dtype and x.shape[-1] % 4 == 0 and x.shape[-1] <= 2048:
-            # one HIP pass: RMSNorm + modulate with the eager op sequence's roundings (jit_thc::norm_modulate)
-            y, _ = ops.norm_modulate(x, self.norm_final.weight, shift.contiguous(), scale.contiguous(), self.norm_final.eps)
-            return self.linear(y)
-        return self.linear(modulate(self.norm_final(x), shift, scale))
+        return self.linear(norm_modulate(self.norm_final, x, shift, scale))
 
 
 class SharedReadLocalTHCSharedAdaLNJiTBlock(nn.Module):
