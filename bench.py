@@ -569,7 +569,7 @@ def main():
             "pct_of_peak_hbm": round(100.0 * value * 1e9 / PEAK_HBM, 2),
         },
         "roofline": {
-            "kernel": "materialise_kernel<bf16 x, fp32 w, L=12> (jit_thc::final_accumulate_b4_12_traceable)",
+            "kernel": "cell_mat_kernel<bf16 x, fp32 w, L=12> (jit_thc::final_accumulate_b4_12_traceable)",
             "bound": "hbm",
             "achieved": round(mat_achieved / 1e9, 2),
             "peak": PEAK_HBM / 1e9,
