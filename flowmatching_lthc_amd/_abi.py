@@ -35,6 +35,9 @@ EXPORTS = (
     "lthc_recur_fwd",
     "lthc_recur_bwd_workspace_bytes",
     "lthc_recur_bwd",
+    "lthc_ws_accumulate_fwd",
+    "lthc_ws_accumulate_bwd_workspace_bytes",
+    "lthc_ws_accumulate_bwd",
     "lthc_norm_modulate_fwd",
     "lthc_norm_modulate_bwd_workspace_bytes",
     "lthc_norm_modulate_bwd",
@@ -72,6 +75,8 @@ def load() -> ctypes.CDLL:
         "lthc_gamma": [vp, pp, ci, vp, ci, i64, i64, ci, vp],
         "lthc_recur_fwd": [vp, vp, ci, vp, ci, vp, i64, i64, vp],
         "lthc_recur_bwd": [vp, vp, vp, ci, vp, ci, vp, vp, i64, i64, vp, sz, vp],
+        "lthc_ws_accumulate_fwd": [vp, pp, ci, vp, ci, vp, i64, i64, ci, vp],
+        "lthc_ws_accumulate_bwd": [vp, pp, ci, vp, ci, pp, vp, i64, i64, ci, vp, sz, vp],
         "lthc_norm_modulate_fwd": [vp, ci, vp, vp, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp],
         "lthc_norm_modulate_bwd": [vp, vp, ci, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, vp, sz, vp],
     }
@@ -83,6 +88,8 @@ def load() -> ctypes.CDLL:
     lib.lthc_weight_grad_workspace_bytes.restype = sz
     lib.lthc_recur_bwd_workspace_bytes.argtypes = [i64, i64]
     lib.lthc_recur_bwd_workspace_bytes.restype = sz
+    lib.lthc_ws_accumulate_bwd_workspace_bytes.argtypes = [i64, i64, ci]
+    lib.lthc_ws_accumulate_bwd_workspace_bytes.restype = sz
     lib.lthc_norm_modulate_bwd_workspace_bytes.argtypes = [i64, i64, i64]
     lib.lthc_norm_modulate_bwd_workspace_bytes.restype = sz
     _lib = lib
@@ -133,3 +140,7 @@ def recur_bwd_workspace_bytes(rows: int, C: int) -> int:
 
 def norm_modulate_bwd_workspace_bytes(B: int, N: int, C: int) -> int:
     return int(load().lthc_norm_modulate_bwd_workspace_bytes(B, N, C))
+
+
+def ws_accumulate_bwd_workspace_bytes(rows: int, C: int, L: int) -> int:
+    return int(load().lthc_ws_accumulate_bwd_workspace_bytes(rows, C, L))

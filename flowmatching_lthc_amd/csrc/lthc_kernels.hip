@@ -1225,20 +1225,22 @@ void launch_cell_mat(const void* base, const PtrPack& dz, const PtrPack& beta, v
 template <int DT, int WDT, int LMAX>
 void launch_cell_mat_l(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells,
                        int G, int C, hipStream_t st) {
-  if (L == LMAX) launch_cell_mat<DT, WDT, LMAX, true, true>(base, dz, beta, out, L, ncells, G, C, st);
-  else launch_cell_mat<DT, WDT, LMAX, true, false>(base, dz, beta, out, L, ncells, G, C, st);
+  if (base == nullptr) {  // the sum of writes alone (the adjoint of a multi-weight read)
+    if (L == LMAX) launch_cell_mat<DT, WDT, LMAX, false, true>(base, dz, beta, out, L, ncells, G, C, st);
+    else launch_cell_mat<DT, WDT, LMAX, false, false>(base, dz, beta, out, L, ncells, G, C, st);
+  } else if (L == LMAX) {
+    launch_cell_mat<DT, WDT, LMAX, true, true>(base, dz, beta, out, L, ncells, G, C, st);
+  } else {
+    launch_cell_mat<DT, WDT, LMAX, true, false>(base, dz, beta, out, L, ncells, G, C, st);
+  }
 }
 
 template <int DT, int WDT>
 void launch_materialise(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells,
                         int G, int C, hipStream_t st) {
   const bool off32 = fits32(ncells * kK * C * Fmt<DT>::bytes);
-  if (base == nullptr) {  // the plain write: one layer, no base (validated by the caller)
-    if (off32) {
-      launch_cell_mat<DT, WDT, 1, false, true>(base, dz, beta, out, 1, ncells, G, C, st);
-    } else {
-      launch_mat_t<DT, WDT, 1, 4, 4, false, true, true, int64_t>(base, dz, beta, out, 1, ncells, G, C, kMatBlocksPerCU, st);
-    }
+  if (base == nullptr && !off32) {  // the plain write, tensors of 4 GiB and more: one layer (validated by the caller)
+    launch_mat_t<DT, WDT, 1, 4, 4, false, true, true, int64_t>(base, dz, beta, out, 1, ncells, G, C, kMatBlocksPerCU, st);
     return;
   }
   if (off32 && L <= kCellMaxDepth) {  // whole-cell kernel: weights of every tap in VGPRs
@@ -1441,7 +1443,8 @@ int lthc_materialise_fwd(const void* base, const void* const* dz, int x_dtype, c
   if (int rc = check_geom(fn, B, G, s, C)) return rc;
   if (int rc = check_layers(fn, L)) return rc;
   if (int rc = check_pair(fn, x_dtype, w_dtype)) return rc;
-  if (base == nullptr && L != 1) return fail(LTHC_ERR_UNSUPPORTED, fn, "base == NULL is implemented for L == 1 only");
+  if (base == nullptr && L != 1 && (L > kCellMaxDepth || !fits32(B * G * G * kK * C * esize(x_dtype))))
+    return fail(LTHC_ERR_UNSUPPORTED, fn, "base == NULL is implemented for L == 1, or L <= 24 below 4 GiB");
   if (B == 0) return LTHC_OK;
   if (base != nullptr)
     if (int rc = check_act(fn, base, x_dtype, "base")) return rc;
@@ -1596,3 +1599,6 @@ int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dty
 
 // Final-layer RMSNorm + modulate of the decoder input (the materialisation's consumer).
 #include "norm_modulate.inc"
+
+// Workspace accumulation of the non-shared (triangular lazy) interface.
+#include "ws_accumulate.inc"

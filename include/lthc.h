@@ -91,7 +91,10 @@ int lthc_read_multi_fwd(const void* g, int x_dtype, const void* const* w, int w_
 /*
  * MATERIALISE / WRITE
  *   out[b,m,k,c] = base[b,m,k,c] + sum_{l<L} beta_l[c,k] * dz_l[b,m,c]
- * `base` may be NULL (treated as zero) when L == 1 — the plain write.  `dz`
+ * `base` may be NULL (treated as zero) when L == 1 — the plain write — and for
+ * L <= 24 when the tensors are below 4 GiB (the sum of writes, which is the
+ * adjoint of a multi-weight read: jit_thc::all_base_b4_12_grad_x,
+ * local_thc_triton_kernels.py:2532-2550).  `dz`
  * and `beta` are host arrays of L
  * device pointers ([B,M,C] and [C,K]).  Accumulation: acc = base, then
  * acc = fma(beta_l, dz_l, acc) for l = 0..L-1, one rounding at the store.
@@ -156,6 +159,30 @@ size_t lthc_recur_bwd_workspace_bytes(int64_t rows, int64_t C);
 int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dtype, const void* gamma,
                    int g_dtype, void* gdz, float* ggamma, int64_t rows, int64_t C,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * WORKSPACE ACCUMULATION (non-shared / triangular lazy interface)
+ *   out[r,c] = base[r,c] + sum_{i<L} gamma[i,c] * dz_i[r,c]        gamma [L, C], L <= 24
+ * With a separate read per layer, layer l's workspace input is
+ * z_l = R_l(x0) + sum_{j<l} gamma[l,j] * dz_j (local_thc.py:1434-1451).
+ * Replaces jit_thc::triangular_accumulate_traceable, the 12-pointer and
+ * active-prefix forms (local_thc_triton_kernels.py:684-711, 1922-2488).
+ * `dz` is a host array of L device pointers; fp32 accumulation, one rounding.
+ */
+int lthc_ws_accumulate_fwd(const void* base, const void* const* dz, int x_dtype, const void* gamma, int g_dtype,
+                           void* out, int64_t rows, int64_t C, int L, void* stream);
+
+/*
+ * Its backward, given g = dL/dout:
+ *   gdz_i[r,c] = gamma[i,c] * g[r,c]       (x_dtype; skipped when gdz is NULL)
+ *   ggamma[i,c] = sum_r g[r,c] * dz_i[r,c] (fp32 [L,C], deterministic; skipped when NULL)
+ * (dL/dbase = g itself.)  Replaces the _grad_dz / _grad_gamma ops of the same
+ * family (:713-762).  The workspace is needed only for ggamma.
+ */
+size_t lthc_ws_accumulate_bwd_workspace_bytes(int64_t rows, int64_t C, int L);
+int lthc_ws_accumulate_bwd(const void* g, const void* const* dz, int x_dtype, const void* gamma, int g_dtype,
+                           void* const* gdz, float* ggamma, int64_t rows, int64_t C, int L, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /*
  * FINAL-LAYER RMSNORM + ADALN MODULATE (the consumer of the materialisation)

@@ -32,6 +32,9 @@ read_multi / Cread_m   ``torch.autograd`` of the materialisation w.r.t. each dZ_
 interface_bwd_np       ``torch.autograd`` of the whole lazy interface (float64), and
                        ``torch.autograd.gradcheck`` of the torch restatement
 recur_bwd              ``torch.autograd`` of z + gamma * dz
+triangular_lazy_np     z_l == R_l(X0 + sum_{j<l} P_j dZ_j) with separate R_l / P_j per layer
+(triangular_np,        (depthwise-conv reads of the naively materialised stream), for every l;
+gamma_matrix_np)       gamma[l, j] == R_l P_j on random data; dropped or extra j caught
 =====================  ==================================================================
 
 Plausible mistakes (swapped sy/sx, transposed weight [K,C] vs [C,K], dropped
@@ -138,6 +141,30 @@ def lazy_forward_np(x0, alpha, dz_list, beta_list, g):
     for dz, beta in zip(dz_list, beta_list, strict=True):
         z = lazy_update_np(z, dz, gamma_np(alpha, beta))
         zs.append(z)
+    return zs, final_accumulate_np(x0, dz_list, beta_list)
+
+
+def gamma_matrix_np(alpha_list, beta_list) -> np.ndarray:
+    """gamma[l, j, c] = sum_k alpha_l[c,k] beta_j[c,k] (local_thc.py:1496; lthc_v2/model.py:257)."""
+    a = np.stack([np.asarray(x, np.float64) for x in alpha_list])
+    b = np.stack([np.asarray(x, np.float64) for x in beta_list])
+    return (a[:, None, :, :] * b[None, :, :, :]).sum(-1)
+
+
+def triangular_np(base: np.ndarray, dz_list, gamma_rows) -> np.ndarray:
+    """triangular_accumulate: base + sum_{i < len(dz_list)} gamma_rows[i] * dz_i
+    (local_thc_triton_kernels.py:1922-2012; the active-prefix forms :2161-2488 use the first `active` layers)."""
+    out = np.asarray(base, np.float64).copy()
+    for i, dz in enumerate(dz_list):
+        out = out + np.asarray(gamma_rows[i], np.float64)[None, None, :] * np.asarray(dz, np.float64)
+    return out
+
+
+def triangular_lazy_np(x0, alpha_list, beta_list, dz_list, g):
+    """Workspace inputs z_l of the non-shared lazy schedule (local_thc.py:1495-1510;
+    lthc_v2/model.py:256-267): z_l = R_l(x0) + sum_{j<l} gamma[l, j] dz_j, and X_L."""
+    gam = gamma_matrix_np(alpha_list, beta_list)
+    zs = [triangular_np(read_np(x0, alpha_list[l], g), dz_list[:l], gam[l]) for l in range(len(alpha_list))]
     return zs, final_accumulate_np(x0, dz_list, beta_list)
 
 

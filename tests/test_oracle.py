@@ -145,6 +145,55 @@ def test_lazy_recurrence_equals_naive_reads():
     np.testing.assert_allclose(xl, x, rtol=1e-12, atol=1e-12)
 
 
+def _triangular_case(L=4, g=4, c=6, seed=3):
+    rng = np.random.default_rng(seed)
+    x0 = rng.standard_normal((2, 4 * g, 4 * g, c))
+    alphas = [rng.standard_normal((c, 16)) * 0.1 + 1 / 16 for _ in range(L)]
+    betas = [rng.standard_normal((c, 16)) for _ in range(L)]
+    dzs = [rng.standard_normal((2, g * g, c)) for _ in range(L)]
+    return x0, alphas, betas, dzs, g
+
+
+def _naive_nonshared_reads(x0, alphas, betas, dzs, g):
+    """z_l = R_l(X_{l}) of the materialised stream X_l = X0 + sum_{j<l} P_j dZ_j (depthwise convs)."""
+    x, zs = x0, []
+    for l in range(len(alphas)):
+        zs.append(conv_read(x, alphas[l], g).numpy())
+        x = x + conv_write(dzs[l], betas[l], 4 * g).numpy()
+    return zs, x
+
+
+def test_gamma_matrix_is_read_of_write():
+    """gamma[l, j] * dZ == R_l(P_j(dZ)) for every (l, j), including l != j."""
+    _, alphas, betas, dzs, g = _triangular_case(L=3)
+    gam = O.gamma_matrix_np(alphas, betas)
+    for l in range(3):
+        for j in range(3):
+            lhs = conv_read(conv_write(dzs[0], betas[j], 4 * g), alphas[l], g).numpy()
+            np.testing.assert_allclose(lhs, gam[l, j][None, None, :] * dzs[0], rtol=1e-10, atol=1e-12)
+
+
+def test_triangular_lazy_equals_naive_nonshared_reads():
+    """The non-shared lazy schedule (separate R_l, P_j per layer) reproduces the naive high-res recurrence."""
+    x0, alphas, betas, dzs, g = _triangular_case(L=5)
+    zs, xl = O.triangular_lazy_np(x0, alphas, betas, dzs, g)
+    ref_zs, ref_x = _naive_nonshared_reads(x0, alphas, betas, dzs, g)
+    for l in range(5):
+        np.testing.assert_allclose(zs[l], ref_zs[l], rtol=1e-10, atol=1e-11, err_msg=f"layer {l}")
+    np.testing.assert_allclose(xl, ref_x, rtol=1e-12, atol=1e-12)
+
+
+def test_mutation_triangular_off_by_one_is_caught():
+    """Summing j <= l (the diagonal) or j < l - 1 (a dropped term) breaks the identity above."""
+    x0, alphas, betas, dzs, g = _triangular_case(L=4)
+    gam = O.gamma_matrix_np(alphas, betas)
+    ref_zs, _ = _naive_nonshared_reads(x0, alphas, betas, dzs, g)
+    base = conv_read(x0, alphas[2], g).numpy()
+    assert not np.allclose(O.triangular_np(base, dzs[:3], gam[2]), ref_zs[2])
+    assert not np.allclose(O.triangular_np(base, dzs[:1], gam[2]), ref_zs[2])
+    assert not np.allclose(O.triangular_np(base, dzs[:2], gam[:, 2]), ref_zs[2])  # transposed gamma
+
+
 def test_materialise_zero_updates_is_identity():
     x0 = rand(1, 8, 8, 4)
     out = O.final_accumulate_np(x0, [np.zeros((1, 4, 4))] * 3, [rand(4, 16) for _ in range(3)])
