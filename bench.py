@@ -56,10 +56,11 @@ def parse_args():
     p.add_argument("--no-configs", action="store_true", help="skip the BASELINE configuration 2 and 5 legs")
     p.add_argument(
         "--profile",
-        choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model", "train"],
+        choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model", "train", "triangular"],
         help="run only this kernel --steps times at the configured shape (for rocprofv3), plus one plain copy "
         "of X0 (a copy kernel of known size that calibrates the FETCH_SIZE / WRITE_SIZE counters); 'model' runs "
-        "only the LTHC-B/4 forward leg, 'train' only the interface fwd+bwd leg",
+        "only the LTHC-B/4 forward leg, 'train' only the interface fwd+bwd leg, 'triangular' only the non-shared "
+        "interface forward leg",
     )
     return p.parse_args()
 
@@ -264,6 +265,107 @@ def interface_forward(args, torch, dev, ops, B, G, C, L):
     }
 
 
+def triangular_forward(args, torch, dev, B, G, C, L):
+    """The non-shared (triangular lazy) interface forward at one shape: the L bases R_l(x0) in one pass
+    (jit_thc::all_base_b4_12_split_traceable), the L-1 workspace sums z_l = base_l + sum_{j<l} gamma[l,j] dz_j
+    (the active-prefix ops at depth 12, triangular_accumulate_list otherwise) and the materialisation, with
+    synthetic dz_l standing in for the branch.  Graph-replayed over two input sets like interface_forward.
+    Compulsory bytes: bases e(T + LW), sums e*sum_{l=1}^{L-1}(l+2)W, materialise e(2T + LW), plus weights."""
+    from flowmatching_lthc_amd import ops
+    from flowmatching_lthc_amd import ops_triangular as T
+
+    H = 4 * G
+    bf16 = torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(11)
+    alpha_stack = (torch.randn((L, C, 16), generator=gen, device=dev) * 0.01 + 1.0 / 16.0).to(bf16)
+    beta_stack = (torch.randn((L, C, 16), generator=gen, device=dev) * 0.02).to(bf16)
+    betas = list(beta_stack.unbind(0))
+    gamma = T.gamma_matrix(alpha_stack, beta_stack)
+    sets = []
+    for _ in range(2):
+        x0 = torch.randn((B, H, H, C), generator=gen, device=dev).to(bf16)
+        dzs = [(torch.randn((B, G * G, C), generator=gen, device=dev) * 0.02).to(bf16) for _ in range(L)]
+        sets.append((x0, dzs))
+    zero = torch.zeros_like(sets[0][1][0])
+    stream = torch.cuda.current_stream()
+    ws_events = []
+
+    def step(i, timed=False):
+        x0, dzs = sets[i % 2]
+        bases = T.all_base_b4_12_split_traceable(x0, alpha_stack)
+        if timed:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+        zs = [bases[0]]
+        for l in range(1, L):
+            if L == 12:
+                args12 = tuple(dzs[j] if j < l else zero for j in range(12))
+                zs.append(T.triangular_accumulate_b4_12_ptr_active_traceable_ops[l - 1](bases[l], *args12, gamma[l]))
+            else:
+                zs.append(T.triangular_accumulate_list(bases[l], dzs[:l], gamma[l, :l].contiguous()))
+        if timed:
+            e1.record(stream)
+            ws_events.append((e0, e1))
+        xl = ops.final_accumulate_list(x0, dzs, betas)
+        return zs, xl
+
+    for i in range(max(2, args.warmup)):
+        step(i, timed=True)
+    torch.cuda.synchronize()
+    ws_events.clear()
+    for i in range(args.steps):
+        step(i, timed=True)
+    torch.cuda.synchronize()
+    ws_ms = sum(a.elapsed_time(b) for a, b in ws_events) / len(ws_events)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(stream)
+    with torch.cuda.stream(side):
+        for i in range(2):
+            step(i)
+    stream.wait_stream(side)
+    torch.cuda.synchronize()
+    graphs, outs = [], []
+    for i in range(2):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            outs.append(step(i))
+        graphs.append(g)
+    ref = step(0)
+    graphs[0].replay()
+    torch.cuda.synchronize()
+    same = torch.equal(outs[0][1], ref[1]) and all(torch.equal(a, b) for a, b in zip(outs[0][0], ref[0]))
+    for i in range(max(2, args.warmup)):
+        graphs[i % 2].replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        graphs[i % 2].replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / args.steps
+    e, T_, W = 2, B * H * H * C, B * G * G * C
+    wbytes = 2 * 16 * C * L
+    by = {
+        "bases": e * (T_ + L * W) + wbytes,
+        "triangular_sums": sum(e * (l + 2) * W + e * l * C for l in range(1, L)),
+        "materialise": e * (2 * T_ + L * W) + wbytes,
+    }
+    total = sum(by.values())
+    del sets, graphs, outs, ref
+    return {
+        "B": B, "high_grid": H, "workspace_grid": G, "C": C, "L": L,
+        "ms_per_step": round(ms, 4),
+        "GBps": round(total / (ms * 1e-3) / 1e9, 1),
+        "pct_of_peak_hbm": round(100.0 * total / (ms * 1e-3) / PEAK_HBM, 2),
+        "triangular_sums_ms_eager": round(ws_ms, 4),
+        "triangular_sums_GBps": round(by["triangular_sums"] / (ws_ms * 1e-3) / 1e9, 1),
+        "bytes_by_op": by,
+        "graph_equals_eager": same,
+    }  # fmt: skip
+
+
 def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label="configuration 3"):
     """the interface forward + autograd backward at the training shape (B=64, bf16).
 
@@ -425,6 +527,10 @@ def main():
     if args.profile == "train":
         print(json.dumps({"interface_train": interface_train(args, torch, dev, ops)}))
         return
+    if args.profile == "triangular":
+        tri = triangular_forward(args, torch, dev, args.batch, args.grid, args.channels, args.depth)
+        print(json.dumps({"triangular_fwd": tri}))
+        return
     B, G, C, L = args.batch, args.grid, args.channels, args.depth
     H = 4 * G
     bf16 = torch.bfloat16
@@ -536,6 +642,7 @@ def main():
             "config2_fwd": interface_forward(args, torch, dev, ops, 32, 16, 768, 12),
             "config5_fwd": interface_forward(args, torch, dev, ops, 32, 32, 1024, 24),
             "config5_train": interface_train(args, torch, dev, ops, 32, 32, 1024, 24, label="configuration 5"),
+            "triangular_fwd_metric_shape": triangular_forward(args, torch, dev, B, G, C, L),
         }
 
     cpu = None
