@@ -1,7 +1,8 @@
 """LTHC interface modules with the reference's hooks and parameter names.
 
 Mirrors ``SharedLocalRead`` and ``LayerLocalWrite`` of
-flowmatching_lthc/models/local_thc.py:1166-1283: same constructor arguments,
+flowmatching_lthc/models/local_thc.py:1166-1283, and the per-block
+``ChannelwiseLocalTokenHyperConnectionTriton*`` modules of :511-617: same constructor arguments,
 validation messages, parameter names (``read_logits``, ``write_weight``) and
 initial values, same hook methods.  The high-resolution work (read, write,
 write_add) runs through the ``jit_thc`` HIP ops of :mod:`.ops`; the [C,16]
@@ -144,6 +145,104 @@ class LayerLocalWrite(nn.Module):
         if self.group_dim == 1:
             return gamma_g
         return gamma_g[:, None].expand(self.pool_groups, self.group_dim).reshape(self.hidden_size)
+
+
+class ChannelwiseLocalTokenHyperConnectionTriton(nn.Module):
+    """Per-block read and write with one module (local_thc.py:511-561): ``read_logits`` and ``write_weight``
+    [C,16], read = R_softmax(read_logits)(x), write = P_write_weight(dz), both with weight gradients.
+
+    The reference's version only runs the 64x64 / 16x16 geometry; this one takes any grid whose cell side
+    is 4.  It keeps the reference's other restrictions: pool_groups == hidden_size and softmax read weights.
+    """
+
+    def __init__(
+        self,
+        high_grid: int,
+        workspace_grid: int,
+        hidden_size: int,
+        pool_groups: int,
+        use_softmax_write: bool = True,
+        init_read: float = 1.0,
+    ) -> None:
+        super().__init__()
+        if high_grid != ops.S * workspace_grid:
+            raise ValueError(f"LocalTHC HIP ops need cell side {ops.S}: high_grid={high_grid}, workspace_grid={workspace_grid}")
+        if pool_groups != hidden_size:
+            raise ValueError("Triton LocalTHC currently requires pool_groups == hidden_size")
+        if not use_softmax_write:
+            raise ValueError("Triton LocalTHC currently assumes softmax read weights")
+        self.high_grid = high_grid
+        self.workspace_grid = workspace_grid
+        self.hidden_size = hidden_size
+        self.pool_groups = pool_groups
+        self.group_dim = 1
+        self.cell_size = ops.S
+        self.cell_tokens = ops.K
+        self.use_softmax_write = use_softmax_write
+        self.read_logits = nn.Parameter(torch.zeros(hidden_size, self.cell_tokens))
+        self.write_weight = nn.Parameter(torch.full((hidden_size, self.cell_tokens), float(init_read)))
+        self.reset_parameters()
+
+    def reset_parameters(self) -> None:
+        nn.init.constant_(self.read_logits, 0.0)
+        nn.init.constant_(self.write_weight, 1.0)
+
+    def _alpha(self, dtype: torch.dtype) -> torch.Tensor:
+        return F.softmax(self.read_logits.float(), dim=-1).to(dtype=dtype)
+
+    def read_from_residual(self, x: torch.Tensor) -> torch.Tensor:
+        return ops.local_write(x, self._alpha(x.dtype))
+
+    def write_to_residual(self, dz: torch.Tensor) -> torch.Tensor:
+        return ops.local_read(dz, self.write_weight.to(dtype=dz.dtype))
+
+    def read(self, x: torch.Tensor) -> torch.Tensor:
+        return self.read_from_residual(x)
+
+    def write(self, dz: torch.Tensor) -> torch.Tensor:
+        return self.write_to_residual(dz)
+
+
+class ChannelwiseLocalTokenHyperConnectionTritonReadAdd(ChannelwiseLocalTokenHyperConnectionTriton):
+    """The write fused with the outer residual add, x + P(dz) in one pass (local_thc.py:564-571)."""
+
+    def write_to_residual_add(self, dz: torch.Tensor, x_hi: torch.Tensor) -> torch.Tensor:
+        return ops.local_read_add(dz, self.write_weight.to(dtype=dz.dtype), x_hi)
+
+    def write_add(self, dz: torch.Tensor, x_hi: torch.Tensor) -> torch.Tensor:
+        return self.write_to_residual_add(dz, x_hi)
+
+
+class ChannelwiseLocalTokenHyperConnectionTritonFrozen(ChannelwiseLocalTokenHyperConnectionTriton):
+    """Read and fused write-add whose weights get no gradient (local_thc.py:574-594)."""
+
+    def read_from_residual(self, x: torch.Tensor) -> torch.Tensor:
+        return ops.local_write_no_weight_grad(x, self._alpha(x.dtype))
+
+    def write_to_residual_add(self, dz: torch.Tensor, x_hi: torch.Tensor) -> torch.Tensor:
+        return ops.local_read_add_no_weight_grad(dz, self.write_weight.to(dtype=dz.dtype), x_hi)
+
+    def write_to_residual(self, dz: torch.Tensor) -> torch.Tensor:
+        raise NotImplementedError("Use write_to_residual_add for TritonFrozen LocalTHC.")
+
+    def write_add(self, dz: torch.Tensor, x_hi: torch.Tensor) -> torch.Tensor:
+        return self.write_to_residual_add(dz, x_hi)
+
+
+class ChannelwiseLocalTokenHyperConnectionTritonTraceable(ChannelwiseLocalTokenHyperConnectionTriton):
+    """Read and fused write-add through the ``jit_thc`` ops, with weight gradients (local_thc.py:597-617)."""
+
+    def read_from_residual(self, x: torch.Tensor) -> torch.Tensor:
+        return ops.local_write_traceable(x, self._alpha(x.dtype))
+
+    def write_to_residual_add(self, dz: torch.Tensor, x_hi: torch.Tensor) -> torch.Tensor:
+        return ops.local_read_add_traceable(dz, self.write_weight.to(dtype=dz.dtype), x_hi)
+
+    def write_to_residual(self, dz: torch.Tensor) -> torch.Tensor:
+        raise NotImplementedError("Use write_to_residual_add for TritonTraceable LocalTHC.")
+
+    def write_add(self, dz: torch.Tensor, x_hi: torch.Tensor) -> torch.Tensor:
+        return self.write_to_residual_add(dz, x_hi)
 
 
 # Backward-compatible aliases (local_thc.py:1426-1427).

@@ -300,6 +300,64 @@ def _backward_read_add(ctx, grad_out):
 torch.library.register_autograd(local_read_add_traceable, _backward_read_add, setup_context=_setup_read_add_ctx)
 
 
+# ---------------------------------------------------------------------------
+# Legacy per-block functions (local_thc_triton_kernels.py:1379-1575): the same
+# maps as the ops above, plus "frozen" forms whose weights get no gradient
+# ---------------------------------------------------------------------------
+class _ReadNoWeightGrad(torch.autograd.Function):
+    """z = R_weight(x); backward dX = R^T(gz) only (_LocalWriteNoWeightGradFunction, :1417-1447)."""
+
+    @staticmethod
+    def forward(ctx, x: Tensor, weight: Tensor) -> Tensor:
+        ctx.save_for_backward(weight)
+        return local_write_traceable(x, weight)
+
+    @staticmethod
+    def backward(ctx, grad_z: Tensor):
+        (weight,) = ctx.saved_tensors
+        return local_read_traceable(grad_z.contiguous(), weight), None
+
+
+class _WriteAddNoWeightGrad(torch.autograd.Function):
+    """x + P_weight(z); backward (R(g), None, g) (_LocalReadAddNoWeightGradFunction, :1525-1555)."""
+
+    @staticmethod
+    def forward(ctx, z: Tensor, weight: Tensor, x: Tensor) -> Tensor:
+        ctx.save_for_backward(weight)
+        return local_read_add_traceable(z, weight, x)
+
+    @staticmethod
+    def backward(ctx, grad_out: Tensor):
+        (weight,) = ctx.saved_tensors
+        grad_out = grad_out.contiguous()
+        return local_write_traceable(grad_out, weight), None, grad_out
+
+
+def local_write(x: Tensor, weight: Tensor) -> Tensor:
+    """The read R_weight(x) with gradients for x and weight (local_thc_triton_kernels.py:1558-1559)."""
+    return local_write_traceable(x, weight)
+
+
+def local_read(z: Tensor, weight: Tensor) -> Tensor:
+    """The write P_weight(z) with gradients for z and weight (:1562-1563)."""
+    return local_read_traceable(z, weight)
+
+
+def local_write_no_weight_grad(x: Tensor, weight: Tensor) -> Tensor:
+    """The read with a frozen weight: no weight gradient (:1566-1567)."""
+    return _ReadNoWeightGrad.apply(x, weight)
+
+
+def local_read_add(z: Tensor, weight: Tensor, x: Tensor) -> Tensor:
+    """x + P_weight(z) in one pass, gradients for all three (:1570-1571)."""
+    return local_read_add_traceable(z, weight, x)
+
+
+def local_read_add_no_weight_grad(z: Tensor, weight: Tensor, x: Tensor) -> Tensor:
+    """x + P_weight(z) with a frozen weight (:1574-1575)."""
+    return _WriteAddNoWeightGrad.apply(z, weight, x)
+
+
 class _OpenInterface(torch.autograd.Function):
     """(x, Z0 = R(x)) as one autograd node.
 

@@ -9,6 +9,7 @@ and decoder; tests/test_gpu_model.py runs the same fixture through the HIP ops.
 """
 
 import os
+import re
 
 import pytest
 import torch
@@ -153,3 +154,79 @@ def test_wrong_image_size_raises():
     m = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG)
     with pytest.raises(ValueError, match="expected image size"):
         m.x_embedder(torch.zeros(1, 3, 16, 16))
+
+
+# ---------------------------------------------------------------------------
+# checkpoint format (scripts/train_imagenet256.py:79-94, flowmatching_lthc/checkpoint.py)
+# ---------------------------------------------------------------------------
+def _legacy(sd):
+    """The same state with the old research key names (the inverse of the migration)."""
+    out = {}
+    for k, v in sd.items():
+        k = k.replace("shared_read.", "shared_write.").replace(".read_logits", ".write_logits")
+        k = re.sub(r"blocks\.(\d+)\.write\.", r"blocks.\1.read.", k).replace(".write_weight", ".read_weight")
+        out[k] = v
+    return out
+
+
+def test_checkpoint_round_trip_with_legacy_keys(tmp_path):
+    from flowmatching_lthc_amd import checkpoint as CK
+
+    fx = load_fixture()
+    src = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG)
+    src.load_state_dict(fx["state_dict"])
+    opt = torch.optim.AdamW(src.parameters(), lr=1e-4)
+    ema = [p.detach() * 0.5 for p in src.parameters()]
+    path = tmp_path / "ckpt.pt"
+    CK.save_checkpoint(path, src, opt, ema, 1234, {"model": "tiny", "prediction": "velocity"})
+    ck = CK.load_checkpoint(path)
+    assert set(ck) == set(CK.CHECKPOINT_KEYS) and ck["step"] == 1234
+    assert ck["meta"]["model"] == "tiny" and ck["meta"]["image_size"] == CONFIG["input_size"]
+
+    # the full state, written with the old key names, loads strictly after migration
+    dst = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG)
+    ck_old = dict(ck, model=_legacy(ck["model"]), ema=_legacy(ck["ema"]))
+    assert "shared_write.write_logits" in ck_old["model"]
+    assert CK.load_model_state(dst, ck_old, key="model") == []
+    for k, v in src.state_dict().items():
+        assert torch.equal(dst.state_dict()[k], v), k
+
+    # EMA: parameters come from the EMA, buffers stay the model's own
+    kept = CK.load_model_state(dst, ck_old, key="ema")
+    params = dict(src.named_parameters())
+    assert set(kept) == set(dst.state_dict()) - set(params)
+    for (n, p), e in zip(dst.named_parameters(), ema):
+        assert torch.equal(p.detach(), e), n
+    with pytest.raises(ValueError):
+        CK.load_model_state(dst, ck, key="optimizer")
+    with pytest.raises(KeyError):
+        CK.load_model_state(dst, {"model": ck["model"]}, key="ema")
+
+
+def test_checkpoint_loader_refuses_pickled_objects(tmp_path):
+    """Checkpoints load with the weights-only loader: an arbitrary pickled object is refused, not run."""
+    from flowmatching_lthc_amd import checkpoint as CK
+
+    path = tmp_path / "bad.pt"
+    torch.save({"model": {}, "obj": _Opaque()}, path)
+    with pytest.raises(Exception):
+        CK.load_checkpoint(path)
+
+
+class _Opaque:
+    pass
+
+
+def test_legacy_hyper_connection_modules_on_cpu():
+    """Parameter names and initial values follow local_thc.py:511-551; the HIP ops refuse CPU tensors."""
+    from flowmatching_lthc_amd import local_thc as LT
+
+    m = LT.ChannelwiseLocalTokenHyperConnectionTritonReadAdd(64, 16, 32, 32)
+    assert [n for n, _ in m.named_parameters()] == ["read_logits", "write_weight"]
+    assert not m.read_logits.any() and bool((m.write_weight == 1).all())
+    with pytest.raises(ValueError):
+        LT.ChannelwiseLocalTokenHyperConnectionTriton(64, 16, 32, 16)
+    with pytest.raises(ValueError):
+        LT.ChannelwiseLocalTokenHyperConnectionTriton(64, 16, 32, 32, use_softmax_write=False)
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        m.read(torch.zeros(1, 64, 64, 32))
