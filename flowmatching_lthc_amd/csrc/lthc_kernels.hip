@@ -635,8 +635,6 @@ __global__ __launch_bounds__(kBlock) void wgrad_partial_kernel(const void* __res
   }
 }
 
-// Zero fill by a kernel rather than hipMemsetAsync, so that callers may
-// capture these launches in a HIP graph.
 // ---------------------------------------------------------------------------
 // WHOLE-CELL MULTI-WEIGHT READ (depth <= 24, tensors below 4 GiB):
 //   out_l[cell,c] = sum_k w_l[c,k] g[cell,k,c]
@@ -644,10 +642,12 @@ __global__ __launch_bounds__(kBlock) void wgrad_partial_kernel(const void* __res
 // group; the weights stay in VGPRs.  Block = LG groups x 256 / LG lanes (a
 // wavefront lies in one group), so each g run is loaded once per layer group
 // (once per cell when LG = 1).  Grid and cell order as cell_mat_kernel.
-// Padding layers (l >= L) load layer 0's weights and are never stored.
+// Padding layers (l >= L) load layer 0's weights and are never stored; with
+// EXACT (L == LMAX) the kernel carries no layer masks.  The L outputs are
+// written with streaming (non-temporal) stores, as are the materialise's.
 // Accumulation order k = 0..15 (local_thc_triton_kernels.py:580-592).
 // ---------------------------------------------------------------------------
-template <int DT, int WDT, int LMAX, int CPT, int LG>
+template <int DT, int WDT, int LMAX, int CPT, int LG, bool EXACT>
 __global__ __launch_bounds__(kBlock) void cell_read_multi_kernel(const void* __restrict__ g, PtrPack w, PtrPack out,
                                                                  int L, uint32_t ncells, int G, int C) {
   constexpr int ES = Fmt<DT>::bytes;
@@ -658,13 +658,13 @@ __global__ __launch_bounds__(kBlock) void cell_read_multi_kernel(const void* __r
   const int c0 = (blockIdx.y * QL + (threadIdx.x - lg * QL)) * CPT;
   const int l0 = lg * LPG;
   uint32_t cell = blockIdx.x;
-  if (c0 >= C || cell >= ncells || l0 >= L) return;
+  if (c0 >= C || cell >= ncells || (!EXACT && l0 >= L)) return;
   float wr[LPG][CPT][kK];
 #pragma unroll
   for (int i = 0; i < LPG; ++i)
 #pragma unroll
     for (int v = 0; v < CPT; ++v)
-      load_wvec<WDT, kK>(w.p[l0 + i < L ? l0 + i : 0], static_cast<int64_t>(c0 + v) * kK, wr[i][v]);
+      load_wvec<WDT, kK>(w.p[(EXACT || l0 + i < L) ? l0 + i : 0], static_cast<int64_t>(c0 + v) * kK, wr[i][v]);
   const uint32_t tap_b = C * ES;
   const uint32_t row_b = G * kS * tap_b;
   const uint32_t P = gridDim.x;
@@ -693,7 +693,7 @@ __global__ __launch_bounds__(kBlock) void cell_read_multi_kernel(const void* __r
     }
 #pragma unroll
     for (int i = 0; i < LPG; ++i)
-      if (l0 + i < L) store_at<DT, CPT>(const_cast<void*>(out.p[l0 + i]), zo, acc[i]);
+      if (EXACT || l0 + i < L) store_at<DT, CPT, true>(const_cast<void*>(out.p[l0 + i]), zo, acc[i]);
   }
 }
 
@@ -1323,8 +1323,9 @@ template <int DT, int WDT, int LMAX>
 void launch_cell_read_multi(const void* g, const PtrPack& w, const PtrPack& out, int L, int64_t ncells, int G, int C,
                             hipStream_t st) {
   constexpr int CPT = CellMatShape<DT, LMAX>::CPT, GR = CellMatShape<DT, LMAX>::GR;
-  const auto kernel = cell_read_multi_kernel<DT, WDT, LMAX, CPT, GR>;
-  static const int per_cu = resident_blocks(kernel);
+  const auto kernel = L == LMAX ? cell_read_multi_kernel<DT, WDT, LMAX, CPT, GR, true>
+                                : cell_read_multi_kernel<DT, WDT, LMAX, CPT, GR, false>;
+  static const int per_cu = resident_blocks(cell_read_multi_kernel<DT, WDT, LMAX, CPT, GR, false>);
   const int slabs = (C / CPT + kBlock / GR - 1) / (kBlock / GR);
   const int64_t per = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu / slabs, ncells, G, 1);
   kernel<<<dim3(static_cast<unsigned>(per), slabs), kBlock, 0, st>>>(g, w, out, L, static_cast<uint32_t>(ncells), G, C);
