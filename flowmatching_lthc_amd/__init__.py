@@ -7,7 +7,7 @@ reference's hook methods and parameter names.  Build the HIP library first:
 ``python -m flowmatching_lthc_amd._build``.
 """
 
-from . import ops, ops_triangular
+from . import ops, ops_branch, ops_triangular
 from .local_thc import LayerLocalRead, LayerLocalWrite, SharedLocalRead, SharedLocalWrite
 
-__all__ = ["ops", "ops_triangular", "SharedLocalRead", "LayerLocalWrite", "SharedLocalWrite", "LayerLocalRead"]
+__all__ = ["ops", "ops_branch", "ops_triangular", "SharedLocalRead", "LayerLocalWrite", "SharedLocalWrite", "LayerLocalRead"]

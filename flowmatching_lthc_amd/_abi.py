@@ -41,6 +41,8 @@ EXPORTS = (
     "lthc_norm_modulate_fwd",
     "lthc_norm_modulate_bwd_workspace_bytes",
     "lthc_norm_modulate_bwd",
+    "lthc_qk_norm_rope",
+    "lthc_swiglu",
 )
 
 _lib = None
@@ -78,6 +80,8 @@ def load() -> ctypes.CDLL:
         "lthc_ws_accumulate_fwd": [vp, pp, ci, vp, ci, vp, i64, i64, ci, vp],
         "lthc_ws_accumulate_bwd": [vp, pp, ci, vp, ci, pp, vp, i64, i64, ci, vp, sz, vp],
         "lthc_norm_modulate_fwd": [vp, ci, vp, vp, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp],
+        "lthc_qk_norm_rope": [vp, ci, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp],
+        "lthc_swiglu": [vp, ci, vp, i64, i64, vp],
         "lthc_norm_modulate_bwd": [vp, vp, ci, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, vp, sz, vp],
     }
     for name, args in sig.items():

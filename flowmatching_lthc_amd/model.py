@@ -24,7 +24,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
-from . import ops
+from . import ops, ops_branch
 from .local_thc import LayerLocalWrite, SharedLocalRead
 
 
@@ -196,11 +196,32 @@ class WorkspaceAttention(nn.Module):
         }
         return sdpa_kernel(table[self.attn_backend]) if self.attn_backend in table else nullcontext()
 
+    def _fused_qk(self, qkv: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> bool:
+        """Whether jit_thc::qk_norm_rope covers this call (GPU, head_dim 64, RMSNorm q/k norms, a full RoPE table)."""
+        return (
+            qkv.is_cuda
+            and qkv.dtype in (torch.bfloat16, torch.float16, torch.float32)
+            and self.head_dim == ops_branch.QK_HEAD_DIM
+            and isinstance(self.q_norm, RMSNorm)
+            and isinstance(self.k_norm, RMSNorm)
+            and self.q_norm.eps == self.k_norm.eps
+            and tuple(rope.freqs_cos.shape) == (qkv.shape[1], self.head_dim)
+        )
+
     def forward(self, x: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> torch.Tensor:
         b, n, c = x.shape
-        q, k, v = self.qkv(x).view(b, n, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
-        q = rope(self.q_norm(q))
-        k = rope(self.k_norm(k))
+        qkv = self.qkv(x)
+        if self._fused_qk(qkv, rope):
+            # one HIP pass for q_norm + rope and k_norm + rope, with the eager sequence's roundings
+            qkv5 = qkv.view(b, n, 3, self.num_heads, self.head_dim)
+            q, k = ops_branch.qk_norm_rope(
+                qkv5, self.q_norm.weight, self.k_norm.weight, rope.freqs_cos, rope.freqs_sin, self.q_norm.eps
+            )
+            q, k, v = q.transpose(1, 2), k.transpose(1, 2), qkv5[:, :, 2].transpose(1, 2)
+        else:
+            q, k, v = qkv.view(b, n, 3, self.num_heads, self.head_dim).permute(2, 0, 3, 1, 4).unbind(0)
+            q = rope(self.q_norm(q))
+            k = rope(self.k_norm(k))
         with self._backends():
             o = F.scaled_dot_product_attention(q, k, v, dropout_p=self.attn_drop.p if self.training else 0.0)
         return self.proj_drop(self.proj(o.transpose(1, 2).reshape(b, n, c)))
@@ -217,8 +238,13 @@ class SwiGLUFFN(nn.Module):
         self.ffn_dropout = nn.Dropout(drop)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        gate, value = self.w12(x).chunk(2, dim=-1)
-        return self.w3(self.ffn_dropout(F.silu(gate) * value))
+        h = self.w12(x)
+        if h.is_cuda and h.dtype in (torch.bfloat16, torch.float16, torch.float32) and h.shape[-1] % 16 == 0:
+            act = ops_branch.swiglu(h)  # silu(gate) * value in one HIP pass, eager roundings
+        else:
+            gate, value = h.chunk(2, dim=-1)
+            act = F.silu(gate) * value
+        return self.w3(self.ffn_dropout(act))
 
 
 class WorkspaceSharedAdaLNBranch(nn.Module):

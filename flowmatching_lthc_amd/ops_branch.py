@@ -1,0 +1,167 @@
+"""Fused elementwise ops of the LTHC transformer branch (gfx950 HIP kernels).
+
+The reference evaluates these chains as eager PyTorch ops; they have no
+``jit_thc`` counterpart there.  Each op here is one HIP pass with the eager
+sequence's roundings (fp32 arithmetic, every eager op's result rounded to the
+activation dtype), registered as a ``jit_thc`` custom op:
+
+* ``jit_thc::qk_norm_rope``: ``rope(q_norm(q))`` and ``rope(k_norm(k))`` of
+  ``WorkspaceAttention.forward`` (local_thc.py:246-249; RMSNorm
+  jit_shared_adaln.py:26-30; VisionRotaryEmbeddingFast jit_shared_adaln.py:57-59),
+  taking the qkv projection [B, N, 3, H, 64] and returning q and k as
+  [B, N, H, 64] (the memory layout of the eager result);
+* ``jit_thc::swiglu``: ``F.silu(x1) * x2`` of ``SwiGLUFFN.forward``
+  (local_thc.py:267-269) for the w12 projection [..., 2F].
+
+Their backward recomputes the eager sequence under autograd (the forward's
+values are those of that sequence), so training through them matches the
+eager model's gradients.
+"""
+
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+from torch import Tensor
+
+from . import _abi
+from .ops import _on_device, _on_gpu
+
+QK_HEAD_DIM = 64
+
+
+# ---------------------------------------------------------------------------
+# eager restatements (the backward recomputes these)
+# ---------------------------------------------------------------------------
+def _rms_norm_eager(x: Tensor, weight: Tensor, eps: float) -> Tensor:
+    xf = x.float()
+    return (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps) * weight).to(x.dtype)
+
+
+def _rope_eager(x: Tensor, cos: Tensor, sin: Tensor) -> Tensor:
+    pairs = x.unflatten(-1, (-1, 2))
+    rot = torch.stack((-pairs[..., 1], pairs[..., 0]), dim=-1).flatten(-2)
+    return x * cos.to(x.dtype) + rot * sin.to(x.dtype)
+
+
+def qk_norm_rope_eager(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, sin: Tensor, eps: float):
+    """The eager sequence on qkv [B, N, 3, H, D]: (q, k) as [B, N, H, D] (cos / sin [N, D] broadcast over heads)."""
+    c, s = cos[:, None, :], sin[:, None, :]
+    q = _rope_eager(_rms_norm_eager(qkv[:, :, 0], q_weight, eps), c, s)
+    k = _rope_eager(_rms_norm_eager(qkv[:, :, 1], k_weight, eps), c, s)
+    return q, k
+
+
+def swiglu_eager(x: Tensor) -> Tensor:
+    a, v = x.chunk(2, dim=-1)
+    return F.silu(a) * v
+
+
+# ---------------------------------------------------------------------------
+# jit_thc::qk_norm_rope
+# ---------------------------------------------------------------------------
+def _check_qk(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, sin: Tensor) -> tuple[int, int, int]:
+    if qkv.dim() != 5 or qkv.shape[2] != 3 or qkv.shape[4] != QK_HEAD_DIM:
+        raise ValueError(f"qkv must be [B,N,3,H,{QK_HEAD_DIM}], got {tuple(qkv.shape)}")
+    b, n, _, h, d = qkv.shape
+    if tuple(q_weight.shape) != (d,) or tuple(k_weight.shape) != (d,):
+        raise ValueError(f"q/k norm weights must be [{d}], got {tuple(q_weight.shape)}, {tuple(k_weight.shape)}")
+    if tuple(cos.shape) != (n, d) or tuple(sin.shape) != (n, d):
+        raise ValueError(f"RoPE tables must be [{n},{d}], got {tuple(cos.shape)}, {tuple(sin.shape)}")
+    _abi.code(qkv)
+    return b, n, h
+
+
+@torch.library.custom_op("jit_thc::qk_norm_rope", mutates_args=())
+def qk_norm_rope(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, sin: Tensor, eps: float) -> tuple[Tensor, Tensor]:
+    """(rope(RMSNorm_q(q)), rope(RMSNorm_k(k))) as [B, N, H, 64] in qkv's dtype, one pass over q and k."""
+    _on_gpu(qkv, q_weight, k_weight, cos, sin)
+    b, n, h = _check_qk(qkv, q_weight, k_weight, cos, sin)
+    qkv = qkv.contiguous()
+    qw, kw = q_weight.float().contiguous(), k_weight.float().contiguous()
+    c, s = cos.float().contiguous(), sin.float().contiguous()
+    q = torch.empty((b, n, h, QK_HEAD_DIM), device=qkv.device, dtype=qkv.dtype)
+    k = torch.empty_like(q)
+    with _on_device(qkv):
+        rc = _abi.load().lthc_qk_norm_rope(
+            qkv.data_ptr(), _abi.code(qkv), qw.data_ptr(), kw.data_ptr(), c.data_ptr(), s.data_ptr(), q.data_ptr(),
+            k.data_ptr(), b, n, h, QK_HEAD_DIM, eps, _abi.stream_of(qkv),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_qk_norm_rope")
+    return q, k
+
+
+@qk_norm_rope.register_fake
+def _(qkv, q_weight, k_weight, cos, sin, eps):
+    b, n, _, h, d = qkv.shape
+    return qkv.new_empty((b, n, h, d)), qkv.new_empty((b, n, h, d))
+
+
+def _setup_qk_ctx(ctx, inputs, output):
+    qkv, q_weight, k_weight, cos, sin, eps = inputs
+    ctx.save_for_backward(qkv, q_weight, k_weight, cos, sin)
+    ctx.eps = eps
+
+
+def _backward_qk(ctx, grad_q, grad_k):
+    qkv, q_weight, k_weight, cos, sin = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    with torch.enable_grad():
+        leaves = [t.detach().requires_grad_(bool(r)) for t, r in zip((qkv, q_weight, k_weight), need[:3])]
+        q, k = qk_norm_rope_eager(leaves[0], leaves[1], leaves[2], cos, sin, ctx.eps)
+        outs, grads = [], []
+        for o, g in ((q, grad_q), (k, grad_k)):
+            if g is not None:
+                outs.append(o)
+                grads.append(g)
+        wanted = [t for t in leaves if t.requires_grad]
+        got = torch.autograd.grad(outs, wanted, grads, allow_unused=True) if outs and wanted else []
+    it = iter(got)
+    res = [next(it) if t.requires_grad else None for t in leaves]
+    return res[0], res[1], res[2], None, None, None
+
+
+torch.library.register_autograd(qk_norm_rope, _backward_qk, setup_context=_setup_qk_ctx)
+
+
+# ---------------------------------------------------------------------------
+# jit_thc::swiglu
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("jit_thc::swiglu", mutates_args=())
+def swiglu(x: Tensor) -> Tensor:
+    """silu(x[..., :F]) * x[..., F:] in x's dtype for x [..., 2F], F % 8 == 0."""
+    _on_gpu(x)
+    two_f = x.shape[-1]
+    if two_f % 16 != 0:
+        raise ValueError(f"last dimension {two_f} must be 2F with F a multiple of 8")
+    f = two_f // 2
+    _abi.code(x)
+    x = x.contiguous()
+    if x.data_ptr() % 16 != 0:
+        x = x.clone()
+    out = torch.empty((*x.shape[:-1], f), device=x.device, dtype=x.dtype)
+    rows = x.numel() // two_f
+    with _on_device(x):
+        rc = _abi.load().lthc_swiglu(x.data_ptr(), _abi.code(x), out.data_ptr(), rows, f, _abi.stream_of(x))
+    _abi.check(rc, "lthc_swiglu")
+    return out
+
+
+@swiglu.register_fake
+def _(x):
+    return x.new_empty((*x.shape[:-1], x.shape[-1] // 2))
+
+
+def _setup_swiglu_ctx(ctx, inputs, output):
+    ctx.save_for_backward(inputs[0])
+
+
+def _backward_swiglu(ctx, grad):
+    (x,) = ctx.saved_tensors
+    with torch.enable_grad():
+        xl = x.detach().requires_grad_()
+        (gx,) = torch.autograd.grad(swiglu_eager(xl), (xl,), (grad,))
+    return gx
+
+
+torch.library.register_autograd(swiglu, _backward_swiglu, setup_context=_setup_swiglu_ctx)

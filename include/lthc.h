@@ -209,6 +209,31 @@ int lthc_norm_modulate_bwd(const void* gy, const void* x, int x_dtype, const flo
                            int64_t B, int64_t N, int64_t C, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/*
+ * Q/K RMSNORM + 2-D ROPE of the branch's attention (no reference op: the
+ * reference evaluates WorkspaceAttention.forward's q_norm/k_norm + rope,
+ * local_thc.py:246-249 with RMSNorm jit_shared_adaln.py:26-30 and
+ * VisionRotaryEmbeddingFast jit_shared_adaln.py:57-59, as about twenty
+ * eager passes per block).  For qkv [B, N, 3, H, D] (the projection, x_dtype)
+ * and x = its q or k part:
+ *   n   = r((x * rsqrt(mean_d x^2 + eps)) * weight[d])              weight fp32 [D]
+ *   out = r(r(n * r(cos[n,d])) + r(rot(n) * r(sin[n,d])))           rot(n)_{2i} = -n_{2i+1}, rot(n)_{2i+1} = n_{2i}
+ * written to q_out / k_out [B, N, H, D] (x_dtype); cos / sin are fp32
+ * [N, D]; r = round to x_dtype.  D must be 64.
+ */
+int lthc_qk_norm_rope(const void* qkv, int x_dtype, const float* q_weight, const float* k_weight, const float* cos_table,
+                      const float* sin_table, void* q_out, void* k_out, int64_t B, int64_t N, int64_t H, int64_t D,
+                      float eps, void* stream);
+
+/*
+ * SWIGLU GATE (no reference op: SwiGLUFFN.forward's chunk + silu + mul,
+ * local_thc.py:267-269, three eager passes):
+ *   out[r, f] = r(r(a / (1 + exp(-a))) * v),  a = x[r, f], v = x[r, F + f]
+ * for x [rows, 2F] and out [rows, F] in x_dtype.  F % 8 == 0; x and out
+ * 16-byte aligned.
+ */
+int lthc_swiglu(const void* x, int x_dtype, void* out, int64_t rows, int64_t F, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -57,6 +57,14 @@ def test_argument_errors_are_reported_without_launching():
     assert rc == _abi.ERR_INVALID and "aligned" in msg
     rc, msg = _err(lib.lthc_weight_grad(fake, arr, _abi.F32, fake, 2, 16, 4, 768, 1, None, 0, None))
     assert rc == _abi.ERR_INVALID and "workspace" in msg
+    rc, msg = _err(lib.lthc_qk_norm_rope(fake, _abi.BF16, fake, fake, fake, fake, fake, fake, 2, 256, 12, 32, 1e-6, None))
+    assert rc == _abi.ERR_UNSUPPORTED and "64" in msg
+    rc, msg = _err(lib.lthc_qk_norm_rope(fake, _abi.BF16, None, fake, fake, fake, fake, fake, 2, 256, 12, 64, 1e-6, None))
+    assert rc == _abi.ERR_INVALID and "NULL" in msg
+    rc, msg = _err(lib.lthc_swiglu(fake, _abi.BF16, fake, 16, 12, None))
+    assert rc == _abi.ERR_UNSUPPORTED and "multiple of 8" in msg
+    rc, msg = _err(lib.lthc_swiglu(ctypes.c_void_p(4096 + 8), _abi.BF16, fake, 16, 16, None))
+    assert rc == _abi.ERR_INVALID and "aligned" in msg
 
 
 def test_workspace_sizes_are_consistent():
@@ -75,6 +83,12 @@ def test_ops_refuse_cpu_tensors():
         ops.local_write_traceable(x, w)
     with pytest.raises(ValueError, match="no CPU fallback"):
         ops.final_accumulate_b4_traceable(x, torch.zeros(2, 1, 256, 8), torch.ones(2, 8, 16))
+    from flowmatching_lthc_amd import ops_branch
+
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        ops_branch.swiglu(torch.zeros(4, 32))
+    with pytest.raises(ValueError, match="no CPU fallback"):
+        ops_branch.qk_norm_rope(torch.zeros(1, 4, 3, 2, 64), torch.ones(64), torch.ones(64), torch.ones(4, 64), torch.zeros(4, 64), 1e-6)
 
 
 def test_fake_shapes_propagate_on_meta():

@@ -1,0 +1,161 @@
+"""GPU parity of the fused branch ops (jit_thc::qk_norm_rope, jit_thc::swiglu) against the eager sequences
+they replace (MI355X only).
+
+The eager sequences are the model's own modules (RMSNorm, VisionRotaryEmbeddingFast on the permuted q/k
+views of the projection; chunk + F.silu + mul), so the check covers the exact op chain the kernels stand in
+for.  fp32: max|d| / max|ref| <= 1e-6.  16-bit: the kernels reproduce every eager rounding, so at least
+99 % of the elements are bit-identical and none differs by more than one unit in the last place
+(|d| <= 2^-7 |ref| for bf16, 2^-10 |ref| for fp16) -- a reduction-order difference in the fp32 mean can
+move one rounding.  Gradients (recomputed through the eager sequence) equal the eager model's.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from flowmatching_lthc_amd import model as M
+from flowmatching_lthc_amd import ops_branch as OB
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda:0")
+ULP = {torch.bfloat16: 2.0**-7, torch.float16: 2.0**-10}
+
+
+def check_close(got, ref, dtype, what):
+    got, ref = got.detach().double().cpu(), ref.detach().double().cpu()
+    if dtype == torch.float32:
+        err = ((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30)).item()
+        assert err <= 1e-6, f"{what}: {err:.3e}"
+        return
+    d = (got - ref).abs()
+    same = (d == 0).double().mean().item()
+    assert same >= 0.99, f"{what}: only {same:.4f} of the elements are bit-identical"
+    # one ulp of the operands of the last eager op: where that op cancels (RoPE's add), an intermediate's
+    # one-ulp move is many ulps of the small result, so the bound uses the tensor's RMS as the operand scale
+    rms = ref.pow(2).mean().sqrt().item()
+    bad = (d > ULP[dtype] * (ref.abs() + rms)).sum().item()
+    assert bad == 0, f"{what}: {bad} elements differ by more than one operand ulp"
+
+
+def eager_qk(qkv5, q_norm, k_norm, rope):
+    """The model's eager path: permuted views -> RMSNorm module -> RoPE module, back to [B, N, H, D]."""
+    q, k, _ = qkv5.permute(2, 0, 3, 1, 4).unbind(0)
+    return rope(q_norm(q)).transpose(1, 2), rope(k_norm(k)).transpose(1, 2)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
+def test_qk_norm_rope_matches_eager(dtype):
+    print(f"case dtype={dtype}", flush=True)
+    B, G, H, D = 2, 16, 12, 64
+    N = G * G
+    gen = torch.Generator().manual_seed(0)
+    qkv = (torch.randn((B, N, 3, H, D), generator=gen) * 2.0).to(DEV, dtype)
+    q_norm, k_norm = M.RMSNorm(D), M.RMSNorm(D)
+    with torch.no_grad():
+        q_norm.weight.copy_(torch.randn(D, generator=gen) * 0.2 + 1)
+        k_norm.weight.copy_(torch.randn(D, generator=gen) * 0.2 + 1)
+    rope = M.VisionRotaryEmbeddingFast(D // 2, G)
+    q_norm, k_norm, rope = q_norm.to(DEV), k_norm.to(DEV), rope.to(DEV)
+
+    q, k = OB.qk_norm_rope(qkv, q_norm.weight, k_norm.weight, rope.freqs_cos, rope.freqs_sin, q_norm.eps)
+    assert q.shape == (B, N, H, D) and q.dtype == dtype and q.is_contiguous()
+    rq, rk = eager_qk(qkv, q_norm, k_norm, rope)
+    check_close(q, rq, dtype, "q")
+    check_close(k, rk, dtype, "k")
+    # the op's own eager restatement is the model's sequence
+    eq, ek = OB.qk_norm_rope_eager(qkv, q_norm.weight, k_norm.weight, rope.freqs_cos, rope.freqs_sin, q_norm.eps)
+    assert torch.equal(eq, rq) and torch.equal(ek, rk)
+    # against the exact function in float64 (no intermediate roundings)
+    x = qkv.double()
+    c, s = rope.freqs_cos.double()[:, None], rope.freqs_sin.double()[:, None]
+    for got, part, w in ((q, 0, q_norm.weight), (k, 1, k_norm.weight)):
+        v = x[:, :, part]
+        n = v * torch.rsqrt(v.pow(2).mean(-1, keepdim=True) + 1e-6) * w.double()
+        rot = torch.stack((-n[..., 1::2], n[..., 0::2]), dim=-1).flatten(-2)
+        exact = n * c + rot * s
+        tol = 1e-5 if dtype == torch.float32 else 4 * ULP[dtype]
+        err = ((got.double() - exact).abs().max() / exact.abs().max()).item()
+        assert err <= tol, f"part {part}: {err:.3e} vs exact"
+
+    # gradients equal the eager model's
+    g = torch.Generator().manual_seed(1)
+    gq = torch.randn(q.shape, generator=g).to(DEV, dtype)
+    gk = torch.randn(k.shape, generator=g).to(DEV, dtype)
+    leaves = [qkv.clone().requires_grad_(), q_norm.weight.detach().clone().requires_grad_(), k_norm.weight.detach().clone().requires_grad_()]
+    fq, fk = OB.qk_norm_rope(leaves[0], leaves[1], leaves[2], rope.freqs_cos, rope.freqs_sin, 1e-6)
+    torch.autograd.backward((fq, fk), (gq, gk))
+    eleaves = [qkv.clone().requires_grad_()]
+    q_norm.weight.grad = k_norm.weight.grad = None
+    rq, rk = eager_qk(eleaves[0].view(B, N, 3, H, D), q_norm, k_norm, rope)
+    torch.autograd.backward((rq, rk), (gq, gk))
+    check_close(leaves[0].grad, eleaves[0].grad, dtype, "grad qkv")
+    for got, ref, what in ((leaves[1].grad, q_norm.weight.grad, "grad q weight"), (leaves[2].grad, k_norm.weight.grad, "grad k weight")):
+        err = ((got.double() - ref.double()).abs().max() / ref.double().abs().max()).item()
+        assert err <= 1e-4, f"{what}: {err:.3e}"
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_swiglu_matches_eager(dtype):
+    print(f"case dtype={dtype}", flush=True)
+    gen = torch.Generator().manual_seed(2)
+    x = (torch.randn((4, 256, 2 * 2048), generator=gen) * 3).to(DEV, dtype)
+    out = OB.swiglu(x)
+    assert out.shape == (4, 256, 2048) and out.dtype == dtype
+    ref = OB.swiglu_eager(x)
+    check_close(out, ref, dtype, "swiglu")
+    a, v = x.double().chunk(2, -1)
+    exact = a * torch.sigmoid(a) * v
+    tol = 1e-6 if dtype == torch.float32 else 2 * ULP[dtype]
+    assert ((out.double() - exact).abs().max() / exact.abs().max()).item() <= tol
+    xl = x.clone().requires_grad_()
+    g = torch.randn(out.shape, generator=gen).to(DEV, dtype)
+    OB.swiglu(xl).backward(g)
+    xe = x.clone().requires_grad_()
+    OB.swiglu_eager(xe).backward(g)
+    assert torch.equal(xl.grad, xe.grad)
+    with pytest.raises(ValueError):
+        OB.swiglu(x[..., :24])
+
+
+def test_model_with_fused_branch_equals_eager_branch(monkeypatch):
+    """A model whose heads are 64 wide (the fused path) gives the eager branch's output and gradients (fp32)."""
+    # heads of 64 channels and a SwiGLU width (int(4 * 192 * 2 / 3) = 512) that the fused ops take
+    cfg = dict(input_size=32, patch_size=4, hidden_size=192, depth=2, num_heads=3, num_classes=10, bottleneck_dim=16,
+               workspace_grid=2, attn_backend="math")
+    torch.manual_seed(0)
+    m = M.randomize_parameters(M.SharedReadLocalTHCSharedAdaLNJiT(**cfg), seed=3).to(DEV)
+    gen = torch.Generator().manual_seed(4)
+    x = torch.randn((2, 3, 32, 32), generator=gen).to(DEV)
+    t = torch.rand((2,), generator=gen).to(DEV)
+    y = torch.randint(0, 10, (2,), generator=gen).to(DEV)
+    calls = {"qk": 0, "swiglu": 0}
+    real_qk, real_sw = OB.qk_norm_rope, OB.swiglu
+
+    def count_qk(*a):
+        calls["qk"] += 1
+        return real_qk(*a)
+
+    def count_sw(*a):
+        calls["swiglu"] += 1
+        return real_sw(*a)
+
+    monkeypatch.setattr(OB, "qk_norm_rope", count_qk)
+    monkeypatch.setattr(OB, "swiglu", count_sw)
+    out = m(x, t, y)
+    out.square().mean().backward()
+    grads = {n: p.grad.clone() for n, p in m.named_parameters() if p.grad is not None}
+    assert calls == {"qk": 2, "swiglu": 2}
+    m.zero_grad()
+    monkeypatch.setattr(OB, "qk_norm_rope", OB.qk_norm_rope_eager)
+    monkeypatch.setattr(OB, "swiglu", OB.swiglu_eager)
+    ref = m(x, t, y)
+    ref.square().mean().backward()
+    assert ((out - ref).abs().max() / ref.abs().max()).item() <= 1e-5
+    for n, p in m.named_parameters():
+        if n in grads:
+            scale = p.grad.abs().max().clamp_min(1e-12)
+            assert ((grads[n] - p.grad).abs().max() / scale).item() <= 1e-4, n

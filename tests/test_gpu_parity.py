@@ -381,7 +381,7 @@ def _eager_norm_modulate(x, w, shift, scale, eps=1e-6):
     return n * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1)
 
 
-@pytest.mark.parametrize("dtype,C", [(F32, 768), (BF16, 768), (BF16, 1024), (F32, 260)])
+@pytest.mark.parametrize("dtype,C", [(F32, 768), (BF16, 768), (BF16, 1024), (F32, 260), (torch.float16, 768)])
 def test_norm_modulate_forward_and_backward(dtype, C):
     g = torch.Generator().manual_seed(11)
     B, N = 3, 257
@@ -405,6 +405,10 @@ def test_norm_modulate_forward_and_backward(dtype, C):
         err = (y.double().cpu() - exact).abs().max().item()
         err_eager = (ref_eager.double().cpu() - exact).abs().max().item()
         assert err <= 1.5 * err_eager + 1e-6, (err, err_eager)
+        # the kernel performs the eager sequence's roundings: bit-identical but for rare one-ulp moves where the
+        # fp32 mean is summed in another order
+        same = (y == ref_eager).double().mean().item()
+        assert same >= 0.99, f"only {same:.4f} of y is bit-identical to the eager sequence"
     # backward against torch autograd of the fp64 function
     xr, wr, shr, scr = (t.double().cpu().requires_grad_(True) for t in (x, w, sh, sc))
     inv_r = torch.rsqrt(xr.pow(2).mean(-1, keepdim=True) + 1e-6)
