@@ -43,6 +43,8 @@ EXPORTS = (
     "lthc_norm_modulate_bwd",
     "lthc_qk_norm_rope",
     "lthc_swiglu",
+    "lthc_gate_add_norm_modulate_fwd",
+    "lthc_gate_residual",
 )
 
 _lib = None
@@ -82,6 +84,8 @@ def load() -> ctypes.CDLL:
         "lthc_norm_modulate_fwd": [vp, ci, vp, vp, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp],
         "lthc_qk_norm_rope": [vp, ci, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp],
         "lthc_swiglu": [vp, ci, vp, i64, i64, vp],
+        "lthc_gate_add_norm_modulate_fwd": [vp, vp, vp, ci, vp, vp, vp, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp],
+        "lthc_gate_residual": [vp, vp, vp, ci, vp, i64, i64, i64, vp],
         "lthc_norm_modulate_bwd": [vp, vp, ci, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, vp, sz, vp],
     }
     for name, args in sig.items():

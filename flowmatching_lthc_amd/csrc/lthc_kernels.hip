@@ -27,6 +27,7 @@
 #include <numeric>
 #include <string>
 #include <type_traits>
+#include <utility>
 
 #include "../../include/lthc.h"
 

@@ -117,9 +117,15 @@ class BottleneckPatchEmbedNHWC(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if tuple(x.shape[-2:]) != self.img_size:
             raise ValueError(f"expected image size {self.img_size}, got {tuple(x.shape[-2:])}")
-        # proj2 is a 1x1 convolution: as a linear map over the channels of proj1's output viewed NHWC it writes
-        # the NHWC residual directly (no permute copy of the C-channel tensor)
-        h = self.proj1(x).permute(0, 2, 3, 1)
+        # proj1 has kernel = stride = patch and no bias: a linear map of each non-overlapping patch (channel,
+        # row, column order, the layout of its weight).  proj2 is a 1x1 convolution: a linear map over proj1's
+        # channels.  As two GEMMs over patch rows in NHWC order the residual comes out NHWC directly, with
+        # proj2's bias in the GEMM (no permute copy of the C-channel tensor, no separate bias pass).
+        b, cin = x.shape[:2]
+        p = self.patch_size[0]
+        gh, gw = self.grid_size
+        patches = x.reshape(b, cin, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5).reshape(b, gh, gw, cin * p * p)
+        h = F.linear(patches, self.proj1.weight.view(self.proj1.out_channels, -1))
         return F.linear(h, self.proj2.weight.view(self.proj2.out_channels, -1), self.proj2.bias)
 
 
@@ -270,7 +276,12 @@ class WorkspaceSharedAdaLNBranch(nn.Module):
 
     def forward(self, z: torch.Tensor, t6: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> torch.Tensor:
         sh_a, sc_a, g_a, sh_m, sc_m, g_m = t6.chunk(6, dim=-1)
-        d_attn = g_a.unsqueeze(1) * self.attn(norm_modulate(self.norm1, z, sh_a, sc_a), rope)
+        a = self.attn(norm_modulate(self.norm1, z, sh_a, sc_a), rope)
+        if z.is_cuda and z.dim() == 3 and a.dtype == z.dtype == t6.dtype and z.shape[-1] % 8 == 0 and z.shape[-1] <= 2048:
+            # d_attn = g_a * a, z + d_attn and its pre-norm in one HIP pass; d_attn + g_m * mlp in another
+            d_attn, h = ops_branch.gate_add_norm_modulate(z, a, g_a, self.norm2.weight, sh_m, sc_m, self.norm2.eps)
+            return ops_branch.gate_residual(d_attn, g_m, self.mlp(h))
+        d_attn = g_a.unsqueeze(1) * a
         d_mlp = g_m.unsqueeze(1) * self.mlp(norm_modulate(self.norm2, z + d_attn, sh_m, sc_m))
         return d_attn + d_mlp
 

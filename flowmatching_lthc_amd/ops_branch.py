@@ -11,11 +11,15 @@ activation dtype), registered as a ``jit_thc`` custom op:
   taking the qkv projection [B, N, 3, H, 64] and returning q and k as
   [B, N, H, 64] (the memory layout of the eager result);
 * ``jit_thc::swiglu``: ``F.silu(x1) * x2`` of ``SwiGLUFFN.forward``
-  (local_thc.py:267-269) for the w12 projection [..., 2F].
+  (local_thc.py:267-269) for the w12 projection [..., 2F];
+* ``jit_thc::gate_add_norm_modulate``: ``dz_attn = gate_msa * attn``,
+  ``z_tmp = z + dz_attn`` and ``modulate(norm2(z_tmp), ...)`` of
+  ``WorkspaceSharedAdaLNBranch.forward`` (local_thc.py:319-322);
+* ``jit_thc::gate_residual``: its ``dz_attn + gate_mlp * mlp`` (:322-323).
 
-Their backward recomputes the eager sequence under autograd (the forward's
-values are those of that sequence), so training through them matches the
-eager model's gradients.
+The backward of the first three recomputes the eager sequence under autograd
+(the forward's values are those of that sequence), so training through them
+matches the eager model's gradients; gate_residual's is its closed form.
 """
 
 from __future__ import annotations
@@ -57,6 +61,12 @@ def swiglu_eager(x: Tensor) -> Tensor:
     return F.silu(a) * v
 
 
+def _aligned(t: Tensor) -> Tensor:
+    """Contiguous with a 16-byte aligned start (the kernels use 16-byte vector accesses)."""
+    t = t.contiguous()
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
 # ---------------------------------------------------------------------------
 # jit_thc::qk_norm_rope
 # ---------------------------------------------------------------------------
@@ -77,9 +87,8 @@ def qk_norm_rope(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, s
     """(rope(RMSNorm_q(q)), rope(RMSNorm_k(k))) as [B, N, H, 64] in qkv's dtype, one pass over q and k."""
     _on_gpu(qkv, q_weight, k_weight, cos, sin)
     b, n, h = _check_qk(qkv, q_weight, k_weight, cos, sin)
-    qkv = qkv.contiguous()
-    qw, kw = q_weight.float().contiguous(), k_weight.float().contiguous()
-    c, s = cos.float().contiguous(), sin.float().contiguous()
+    qkv, qw, kw = _aligned(qkv), _aligned(q_weight.float()), _aligned(k_weight.float())
+    c, s = _aligned(cos.float()), _aligned(sin.float())
     q = torch.empty((b, n, h, QK_HEAD_DIM), device=qkv.device, dtype=qkv.dtype)
     k = torch.empty_like(q)
     with _on_device(qkv):
@@ -136,9 +145,7 @@ def swiglu(x: Tensor) -> Tensor:
         raise ValueError(f"last dimension {two_f} must be 2F with F a multiple of 8")
     f = two_f // 2
     _abi.code(x)
-    x = x.contiguous()
-    if x.data_ptr() % 16 != 0:
-        x = x.clone()
+    x = _aligned(x)
     out = torch.empty((*x.shape[:-1], f), device=x.device, dtype=x.dtype)
     rows = x.numel() // two_f
     with _on_device(x):
@@ -165,3 +172,120 @@ def _backward_swiglu(ctx, grad):
 
 
 torch.library.register_autograd(swiglu, _backward_swiglu, setup_context=_setup_swiglu_ctx)
+
+
+# ---------------------------------------------------------------------------
+# gated residuals of the branch: jit_thc::gate_add_norm_modulate, jit_thc::gate_residual
+# (WorkspaceSharedAdaLNBranch.forward, local_thc.py:319-323)
+# ---------------------------------------------------------------------------
+def gate_add_norm_modulate_eager(z: Tensor, a: Tensor, gate: Tensor, weight: Tensor, shift: Tensor, scale: Tensor, eps: float):
+    """(d, y): d = gate * a, y = modulate(RMSNorm(z + d), shift, scale), as the eager branch evaluates them."""
+    d = gate.unsqueeze(1) * a
+    n = _rms_norm_eager(z + d, weight, eps)
+    return d, n * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1)
+
+
+def gate_residual_eager(d: Tensor, gate: Tensor, m: Tensor) -> Tensor:
+    return d + gate.unsqueeze(1) * m
+
+
+def _check_bnc(name: str, t: Tensor, shape: tuple, dtype: torch.dtype) -> None:
+    if tuple(t.shape) != shape or t.dtype != dtype:
+        raise ValueError(f"{name} must be {list(shape)} {dtype}, got {tuple(t.shape)} {t.dtype}")
+
+
+@torch.library.custom_op("jit_thc::gate_add_norm_modulate", mutates_args=())
+def gate_add_norm_modulate(
+    z: Tensor, a: Tensor, gate: Tensor, weight: Tensor, shift: Tensor, scale: Tensor, eps: float
+) -> tuple[Tensor, Tensor]:
+    """(gate * a, modulate(RMSNorm(z + gate * a), shift, scale)) in z's dtype, one pass; z, a [B,N,C], the rest [B,C]
+    (weight [C])."""
+    _on_gpu(z, a, gate, weight, shift, scale)
+    if z.dim() != 3:
+        raise ValueError(f"z must be [B,N,C], got {tuple(z.shape)}")
+    b, n, c = z.shape
+    _check_bnc("a", a, (b, n, c), z.dtype)
+    for name, t in (("gate", gate), ("shift", shift), ("scale", scale)):
+        _check_bnc(name, t, (b, c), z.dtype)
+    if tuple(weight.shape) != (c,):
+        raise ValueError(f"weight must be [{c}], got {tuple(weight.shape)}")
+    _abi.code(z)
+    z, a, gate, shift, scale = (_aligned(t) for t in (z, a, gate, shift, scale))
+    w = _aligned(weight.float())
+    d, y = torch.empty_like(z), torch.empty_like(z)
+    with _on_device(z):
+        rc = _abi.load().lthc_gate_add_norm_modulate_fwd(
+            z.data_ptr(), a.data_ptr(), gate.data_ptr(), _abi.code(z), w.data_ptr(), shift.data_ptr(), scale.data_ptr(),
+            d.data_ptr(), y.data_ptr(), None, b, n, c, eps, _abi.stream_of(z),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_gate_add_norm_modulate_fwd")
+    return d, y
+
+
+@gate_add_norm_modulate.register_fake
+def _(z, a, gate, weight, shift, scale, eps):
+    return torch.empty_like(z), torch.empty_like(z)
+
+
+def _setup_ganm_ctx(ctx, inputs, output):
+    ctx.save_for_backward(*inputs[:6])
+    ctx.eps = inputs[6]
+
+
+def _backward_ganm(ctx, grad_d, grad_y):
+    saved = ctx.saved_tensors
+    need = ctx.needs_input_grad[:6]
+    with torch.enable_grad():
+        leaves = [t.detach().requires_grad_(bool(r)) for t, r in zip(saved, need)]
+        d, y = gate_add_norm_modulate_eager(*leaves, ctx.eps)
+        outs = [o for o, g in ((d, grad_d), (y, grad_y)) if g is not None]
+        grads = [g for g in (grad_d, grad_y) if g is not None]
+        wanted = [t for t in leaves if t.requires_grad]
+        got = torch.autograd.grad(outs, wanted, grads, allow_unused=True) if outs and wanted else []
+    it = iter(got)
+    return (*[next(it) if t.requires_grad else None for t in leaves], None)
+
+
+torch.library.register_autograd(gate_add_norm_modulate, _backward_ganm, setup_context=_setup_ganm_ctx)
+
+
+@torch.library.custom_op("jit_thc::gate_residual", mutates_args=())
+def gate_residual(d: Tensor, gate: Tensor, m: Tensor) -> Tensor:
+    """d + gate * m in d's dtype for d, m [B,N,C] and a per-sample gate [B,C] (C % 8 == 0)."""
+    _on_gpu(d, gate, m)
+    if d.dim() != 3 or d.shape[2] % 8 != 0:
+        raise ValueError(f"d must be [B,N,C] with C % 8 == 0, got {tuple(d.shape)}")
+    b, n, c = d.shape
+    _check_bnc("m", m, (b, n, c), d.dtype)
+    _check_bnc("gate", gate, (b, c), d.dtype)
+    _abi.code(d)
+    d, gate, m = _aligned(d), _aligned(gate), _aligned(m)
+    out = torch.empty_like(d)
+    with _on_device(d):
+        rc = _abi.load().lthc_gate_residual(
+            d.data_ptr(), gate.data_ptr(), m.data_ptr(), _abi.code(d), out.data_ptr(), b, n, c, _abi.stream_of(d)
+        )
+    _abi.check(rc, "lthc_gate_residual")
+    return out
+
+
+@gate_residual.register_fake
+def _(d, gate, m):
+    return torch.empty_like(d)
+
+
+def _setup_gres_ctx(ctx, inputs, output):
+    d, gate, m = inputs
+    ctx.save_for_backward(gate, m)
+
+
+def _backward_gres(ctx, grad):
+    gate, m = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    grad_d = grad if need[0] else None
+    grad_gate = (grad * m).float().sum(1).to(gate.dtype) if need[1] else None
+    grad_m = grad * gate.unsqueeze(1) if need[2] else None
+    return grad_d, grad_gate, grad_m
+
+
+torch.library.register_autograd(gate_residual, _backward_gres, setup_context=_setup_gres_ctx)

@@ -219,7 +219,8 @@ int lthc_norm_modulate_bwd(const void* gy, const void* x, int x_dtype, const flo
  *   n   = r((x * rsqrt(mean_d x^2 + eps)) * weight[d])              weight fp32 [D]
  *   out = r(r(n * r(cos[n,d])) + r(rot(n) * r(sin[n,d])))           rot(n)_{2i} = -n_{2i+1}, rot(n)_{2i+1} = n_{2i}
  * written to q_out / k_out [B, N, H, D] (x_dtype); cos / sin are fp32
- * [N, D]; r = round to x_dtype.  D must be 64.
+ * [N, D]; r = round to x_dtype.  D must be 64; qkv, the outputs, weights
+ * and tables 16-byte aligned.
  */
 int lthc_qk_norm_rope(const void* qkv, int x_dtype, const float* q_weight, const float* k_weight, const float* cos_table,
                       const float* sin_table, void* q_out, void* k_out, int64_t B, int64_t N, int64_t H, int64_t D,
@@ -233,6 +234,23 @@ int lthc_qk_norm_rope(const void* qkv, int x_dtype, const float* q_weight, const
  * 16-byte aligned.
  */
 int lthc_swiglu(const void* x, int x_dtype, void* out, int64_t rows, int64_t F, void* stream);
+
+/*
+ * GATED RESIDUALS OF THE BRANCH (no reference op: WorkspaceSharedAdaLNBranch.forward,
+ * local_thc.py:319-323, evaluates them as eager multiplies and adds).  For
+ * tokens t = b*N + n of [B, N, C] tensors and per-sample [B, C] gates:
+ *   lthc_gate_add_norm_modulate_fwd:  d = r(gate * a),  x = r(z + d),  then the
+ *     RMSNorm + modulate of x as lthc_norm_modulate_fwd (y, inv); d is written
+ *     to d_out.  (dz_attn, z_tmp and the second pre-norm in one pass.)
+ *   lthc_gate_residual:  out = r(d + r(gate * m))   (dz_attn + gate_mlp * mlp);
+ *     C % 8 == 0, every pointer 16-byte aligned.
+ * All tensors in x_dtype except the fp32 weight [C] and inv [B*N] (may be NULL).
+ */
+int lthc_gate_add_norm_modulate_fwd(const void* z, const void* a, const void* gate, int x_dtype, const float* weight,
+                                    const void* shift, const void* scale, void* d_out, void* y, float* inv, int64_t B,
+                                    int64_t N, int64_t C, float eps, void* stream);
+int lthc_gate_residual(const void* d, const void* gate, const void* m, int x_dtype, void* out, int64_t B, int64_t N,
+                       int64_t C, void* stream);
 
 #ifdef __cplusplus
 }

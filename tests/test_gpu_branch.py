@@ -122,7 +122,8 @@ def test_swiglu_matches_eager(dtype):
 
 
 def test_model_with_fused_branch_equals_eager_branch(monkeypatch):
-    """A model whose heads are 64 wide (the fused path) gives the eager branch's output and gradients (fp32)."""
+    """A model whose heads are 64 wide (the fused path) gives the eager branch's output and gradients (fp32);
+    the eager run replaces every fused branch op by its eager sequence."""
     # heads of 64 channels and a SwiGLU width (int(4 * 192 * 2 / 3) = 512) that the fused ops take
     cfg = dict(input_size=32, patch_size=4, hidden_size=192, depth=2, num_heads=3, num_classes=10, bottleneck_dim=16,
                workspace_grid=2, attn_backend="math")
@@ -148,10 +149,12 @@ def test_model_with_fused_branch_equals_eager_branch(monkeypatch):
     out = m(x, t, y)
     out.square().mean().backward()
     grads = {n: p.grad.clone() for n, p in m.named_parameters() if p.grad is not None}
-    assert calls == {"qk": 2, "swiglu": 2}
+    assert calls == {"qk": 2, "swiglu": 2}, calls
     m.zero_grad()
     monkeypatch.setattr(OB, "qk_norm_rope", OB.qk_norm_rope_eager)
     monkeypatch.setattr(OB, "swiglu", OB.swiglu_eager)
+    monkeypatch.setattr(OB, "gate_add_norm_modulate", OB.gate_add_norm_modulate_eager)
+    monkeypatch.setattr(OB, "gate_residual", OB.gate_residual_eager)
     ref = m(x, t, y)
     ref.square().mean().backward()
     assert ((out - ref).abs().max() / ref.abs().max()).item() <= 1e-5
@@ -159,3 +162,39 @@ def test_model_with_fused_branch_equals_eager_branch(monkeypatch):
         if n in grads:
             scale = p.grad.abs().max().clamp_min(1e-12)
             assert ((grads[n] - p.grad).abs().max() / scale).item() <= 1e-4, n
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_gated_residual_ops_match_eager(dtype):
+    print(f"case dtype={dtype}", flush=True)
+    B, N, C = 4, 256, 768
+    gen = torch.Generator().manual_seed(5)
+    z, a, m = (torch.randn((B, N, C), generator=gen).to(DEV, dtype) for _ in range(3))
+    gate, shift, scale = ((torch.randn((B, 6 * C), generator=gen) * 0.3).to(DEV, dtype)[:, :C] for _ in range(3))
+    w = (torch.randn(C, generator=gen) * 0.1 + 1).to(DEV)
+    d, y = OB.gate_add_norm_modulate(z, a, gate, w, shift, scale, 1e-6)
+    rd, ry = OB.gate_add_norm_modulate_eager(z, a, gate, w, shift, scale, 1e-6)
+    assert torch.equal(d, rd), "d = gate * a is one rounded multiply"
+    check_close(y, ry, dtype, "y")
+    # the eager restatement is the model's: modulate(RMSNorm module(z + d))
+    norm = M.RMSNorm(C).to(DEV)
+    with torch.no_grad():
+        norm.weight.copy_(w)
+    assert torch.equal(ry, M.modulate(norm(z + rd), shift, scale))
+    out = OB.gate_residual(d, gate, m)
+    assert torch.equal(out, OB.gate_residual_eager(d, gate, m)) or dtype == torch.float32
+    check_close(out, OB.gate_residual_eager(d, gate, m), dtype, "gate_residual")
+    # gradients through both ops equal the eager sequence's
+    leaves = [t.clone().requires_grad_() for t in (z, a, gate, shift, scale, m)]
+    wl = w.clone().requires_grad_()
+    d1, y1 = OB.gate_add_norm_modulate(leaves[0], leaves[1], leaves[2], wl, leaves[3], leaves[4], 1e-6)
+    (OB.gate_residual(d1, leaves[2], leaves[5]).float().sum() + y1.float().square().sum()).backward()
+    eleaves = [t.clone().requires_grad_() for t in (z, a, gate, shift, scale, m)]
+    we = w.clone().requires_grad_()
+    d2, y2 = OB.gate_add_norm_modulate_eager(eleaves[0], eleaves[1], eleaves[2], we, eleaves[3], eleaves[4], 1e-6)
+    (OB.gate_residual_eager(d2, eleaves[2], eleaves[5]).float().sum() + y2.float().square().sum()).backward()
+    for name, p, q in zip(("z", "a", "gate", "shift", "scale", "m"), leaves, eleaves):
+        err = ((p.grad.double() - q.grad.double()).abs().max() / q.grad.double().abs().max().clamp_min(1e-30)).item()
+        assert err <= (1e-5 if dtype == torch.float32 else 2e-2), f"grad {name}: {err:.3e}"
+    err = ((wl.grad - we.grad).abs().max() / we.grad.abs().max()).item()
+    assert err <= 1e-4, f"grad weight: {err:.3e}"
