@@ -81,12 +81,14 @@ def load() -> ctypes.CDLL:
         "lthc_recur_bwd": [vp, vp, vp, ci, vp, ci, vp, vp, i64, i64, vp, sz, vp],
         "lthc_ws_accumulate_fwd": [vp, pp, ci, vp, ci, vp, i64, i64, ci, vp],
         "lthc_ws_accumulate_bwd": [vp, pp, ci, vp, ci, pp, vp, i64, i64, ci, vp, sz, vp],
-        "lthc_norm_modulate_fwd": [vp, ci, vp, vp, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp],
-        "lthc_qk_norm_rope": [vp, ci, vp, vp, vp, vp, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp],
+        "lthc_norm_modulate_fwd": [vp, ci, vp, ci, vp, vp, i64, vp, vp, i64, i64, i64, ctypes.c_float, vp],
+        "lthc_qk_norm_rope": [vp, ci, vp, vp, ci, vp, vp, ci, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp],
         "lthc_swiglu": [vp, ci, vp, i64, i64, vp],
-        "lthc_gate_add_norm_modulate_fwd": [vp, vp, vp, ci, vp, vp, vp, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp],
-        "lthc_gate_residual": [vp, vp, vp, ci, vp, i64, i64, i64, vp],
-        "lthc_norm_modulate_bwd": [vp, vp, ci, vp, vp, vp, vp, vp, vp, vp, i64, i64, i64, vp, sz, vp],
+        "lthc_gate_add_norm_modulate_fwd": [
+            vp, vp, vp, ci, vp, ci, vp, vp, i64, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp,
+        ],  # fmt: skip
+        "lthc_gate_residual": [vp, vp, i64, vp, ci, vp, i64, i64, i64, vp],
+        "lthc_norm_modulate_bwd": [vp, vp, ci, vp, ci, vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, vp, sz, vp],
     }
     for name, args in sig.items():
         fn = getattr(lib, name)

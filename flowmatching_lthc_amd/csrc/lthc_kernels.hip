@@ -1391,7 +1391,7 @@ extern "C" {
 
 const char* lthc_last_error(void) { return g_last_error.c_str(); }
 
-int lthc_abi_version(void) { return 2; }
+int lthc_abi_version(void) { return 3; }
 
 int lthc_read_fwd(const void* x, int x_dtype, const void* alpha, int w_dtype, void* z, int64_t B, int64_t G, int64_t s,
                   int64_t C, void* stream) {

@@ -55,7 +55,7 @@ def norm_modulate(norm: RMSNorm, x: torch.Tensor, shift: torch.Tensor, scale: to
     follow torch's promotion rules, which the kernel does not implement).
     """
     if x.is_cuda and x.dim() == 3 and shift.dtype == x.dtype and scale.dtype == x.dtype and x.shape[-1] % 4 == 0 and x.shape[-1] <= 2048:
-        return ops.norm_modulate(x, norm.weight, shift.contiguous(), scale.contiguous(), norm.eps)[0]
+        return ops.norm_modulate(x, norm.weight, shift, scale, norm.eps)[0]
     return modulate(norm(x), shift, scale)
 
 

@@ -905,19 +905,42 @@ def _check_norm(x: Tensor, weight: Tensor, shift: Tensor, scale: Tensor) -> tupl
     return b, n, c
 
 
+def _mod_rows(*ts: Tensor, elems: int = 4) -> tuple[list[Tensor], int]:
+    """Per-sample [B, C] vectors as (tensors, common row stride): strided rows of one buffer (chunks of the shared
+    AdaLN vector) are used in place when their rows are contiguous, share a stride that is a multiple of `elems`
+    and start `elems`-element aligned; otherwise each is made contiguous (stride C)."""
+    c = ts[0].shape[1]
+    ld = ts[0].stride(0)
+    ok = all(
+        t.stride(1) == 1 and t.stride(0) == ld and (t.data_ptr() // t.element_size()) % elems == 0 for t in ts
+    ) and ld >= c and ld % elems == 0
+    if ok:
+        return list(ts), ld
+    out = [t.contiguous() for t in ts]
+    out = [t if (t.data_ptr() // t.element_size()) % elems == 0 else t.clone() for t in out]
+    return out, c
+
+
+def _norm_weight(weight: Tensor) -> Tensor:
+    """The RMSNorm weight as passed to the kernels: fp32, bf16 or fp16, contiguous."""
+    w = weight if weight.dtype in (torch.float32, torch.bfloat16, torch.float16) else weight.float()
+    return w.contiguous()
+
+
 @torch.library.custom_op("jit_thc::norm_modulate", mutates_args=())
 def norm_modulate(x: Tensor, weight: Tensor, shift: Tensor, scale: Tensor, eps: float) -> tuple[Tensor, Tensor]:
     """(modulate(RMSNorm(x), shift, scale) in x.dtype, fp32 [B*N] inverse RMS) in one pass over x."""
     _on_gpu(x, weight, shift, scale)
     b, n, c = _check_norm(x, weight, shift, scale)
-    x, shift, scale = _prep(x), _prep(shift), _prep(scale)
-    w = weight.float().contiguous()
+    x = _prep(x)
+    (shift, scale), ld = _mod_rows(shift, scale)
+    w = _norm_weight(weight)
     y = torch.empty_like(x)
     inv = torch.empty((b * n,), device=x.device, dtype=torch.float32)
     with _on_device(x):
         rc = _abi.load().lthc_norm_modulate_fwd(
-            x.data_ptr(), _abi.code(x), w.data_ptr(), shift.data_ptr(), scale.data_ptr(), y.data_ptr(),
-            inv.data_ptr(), b, n, c, eps, _abi.stream_of(x),
+            x.data_ptr(), _abi.code(x), w.data_ptr(), _abi.code(w), shift.data_ptr(), scale.data_ptr(), ld,
+            y.data_ptr(), inv.data_ptr(), b, n, c, eps, _abi.stream_of(x),
         )  # fmt: skip
     _abi.check(rc, "lthc_norm_modulate_fwd")
     return y, inv
@@ -936,8 +959,9 @@ def norm_modulate_backward(
     _on_gpu(grad, x, weight, scale, inv)
     b, n, c = _check_norm(x, weight, scale, scale)
     (grad,) = _same_dtype(x, [_prep(grad)])
-    x, scale, inv = _prep(x), _prep(scale), inv.float().contiguous()
-    w = weight.float().contiguous()
+    x, inv = _prep(x), inv.float().contiguous()
+    (scale,), ld = _mod_rows(scale)
+    w = _norm_weight(weight)
     gx = torch.empty_like(x)
     gw = torch.empty((c,), device=x.device, dtype=torch.float32)
     gsh = torch.empty((b, c), device=x.device, dtype=torch.float32)
@@ -945,9 +969,9 @@ def norm_modulate_backward(
     ws = torch.empty((max(_abi.norm_modulate_bwd_workspace_bytes(b, n, c), 16),), device=x.device, dtype=torch.uint8)
     with _on_device(x):
         rc = _abi.load().lthc_norm_modulate_bwd(
-            grad.data_ptr(), x.data_ptr(), _abi.code(x), w.data_ptr(), scale.data_ptr(), inv.data_ptr(),
-            gx.data_ptr(), gw.data_ptr(), gsh.data_ptr(), gsc.data_ptr(), b, n, c, ws.data_ptr(), ws.numel(),
-            _abi.stream_of(x),
+            grad.data_ptr(), x.data_ptr(), _abi.code(x), w.data_ptr(), _abi.code(w), scale.data_ptr(), ld,
+            inv.data_ptr(), gx.data_ptr(), gw.data_ptr(), gsh.data_ptr(), gsc.data_ptr(), b, n, c, ws.data_ptr(),
+            ws.numel(), _abi.stream_of(x),
         )  # fmt: skip
     _abi.check(rc, "lthc_norm_modulate_bwd")
     return gx, gw, gsh, gsc

@@ -29,7 +29,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import _abi
-from .ops import _on_device, _on_gpu
+from .ops import _mod_rows, _norm_weight, _on_device, _on_gpu
 
 QK_HEAD_DIM = 64
 
@@ -87,14 +87,20 @@ def qk_norm_rope(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, s
     """(rope(RMSNorm_q(q)), rope(RMSNorm_k(k))) as [B, N, H, 64] in qkv's dtype, one pass over q and k."""
     _on_gpu(qkv, q_weight, k_weight, cos, sin)
     b, n, h = _check_qk(qkv, q_weight, k_weight, cos, sin)
-    qkv, qw, kw = _aligned(qkv), _aligned(q_weight.float()), _aligned(k_weight.float())
-    c, s = _aligned(cos.float()), _aligned(sin.float())
+    qkv = _aligned(qkv)
+    # weights and tables: fp32 or the activation dtype (bf16 parameters and buffers are used as they are)
+    qw, kw, c, s = (t if t.dtype == qkv.dtype else t.float() for t in (q_weight, k_weight, cos, sin))
+    if kw.dtype != qw.dtype:
+        qw, kw = qw.float(), kw.float()
+    if s.dtype != c.dtype:
+        c, s = c.float(), s.float()
+    qw, kw, c, s = (_aligned(t) for t in (qw, kw, c, s))
     q = torch.empty((b, n, h, QK_HEAD_DIM), device=qkv.device, dtype=qkv.dtype)
     k = torch.empty_like(q)
     with _on_device(qkv):
         rc = _abi.load().lthc_qk_norm_rope(
-            qkv.data_ptr(), _abi.code(qkv), qw.data_ptr(), kw.data_ptr(), c.data_ptr(), s.data_ptr(), q.data_ptr(),
-            k.data_ptr(), b, n, h, QK_HEAD_DIM, eps, _abi.stream_of(qkv),
+            qkv.data_ptr(), _abi.code(qkv), qw.data_ptr(), kw.data_ptr(), _abi.code(qw), c.data_ptr(), s.data_ptr(),
+            _abi.code(c), q.data_ptr(), k.data_ptr(), b, n, h, QK_HEAD_DIM, eps, _abi.stream_of(qkv),
         )  # fmt: skip
     _abi.check(rc, "lthc_qk_norm_rope")
     return q, k
@@ -210,13 +216,14 @@ def gate_add_norm_modulate(
     if tuple(weight.shape) != (c,):
         raise ValueError(f"weight must be [{c}], got {tuple(weight.shape)}")
     _abi.code(z)
-    z, a, gate, shift, scale = (_aligned(t) for t in (z, a, gate, shift, scale))
-    w = _aligned(weight.float())
+    z, a = _aligned(z), _aligned(a)
+    (gate, shift, scale), ld = _mod_rows(gate, shift, scale)
+    w = _norm_weight(weight)
     d, y = torch.empty_like(z), torch.empty_like(z)
     with _on_device(z):
         rc = _abi.load().lthc_gate_add_norm_modulate_fwd(
-            z.data_ptr(), a.data_ptr(), gate.data_ptr(), _abi.code(z), w.data_ptr(), shift.data_ptr(), scale.data_ptr(),
-            d.data_ptr(), y.data_ptr(), None, b, n, c, eps, _abi.stream_of(z),
+            z.data_ptr(), a.data_ptr(), gate.data_ptr(), _abi.code(z), w.data_ptr(), _abi.code(w), shift.data_ptr(),
+            scale.data_ptr(), ld, d.data_ptr(), y.data_ptr(), None, b, n, c, eps, _abi.stream_of(z),
         )  # fmt: skip
     _abi.check(rc, "lthc_gate_add_norm_modulate_fwd")
     return d, y
@@ -259,11 +266,12 @@ def gate_residual(d: Tensor, gate: Tensor, m: Tensor) -> Tensor:
     _check_bnc("m", m, (b, n, c), d.dtype)
     _check_bnc("gate", gate, (b, c), d.dtype)
     _abi.code(d)
-    d, gate, m = _aligned(d), _aligned(gate), _aligned(m)
+    d, m = _aligned(d), _aligned(m)
+    (gate,), ld = _mod_rows(gate, elems=8)
     out = torch.empty_like(d)
     with _on_device(d):
         rc = _abi.load().lthc_gate_residual(
-            d.data_ptr(), gate.data_ptr(), m.data_ptr(), _abi.code(d), out.data_ptr(), b, n, c, _abi.stream_of(d)
+            d.data_ptr(), gate.data_ptr(), ld, m.data_ptr(), _abi.code(d), out.data_ptr(), b, n, c, _abi.stream_of(d)
         )
     _abi.check(rc, "lthc_gate_residual")
     return out

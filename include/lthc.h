@@ -189,14 +189,17 @@ int lthc_ws_accumulate_bwd(const void* g, const void* const* dz, int x_dtype, co
  *   inv[t]  = rsqrt(mean_c x[t,c]^2 + eps)                           fp32 [B*N] (may be NULL)
  *   y[t,c]  = r(r(r((x*inv)*weight[c]) * r(1 + scale[b,c])) + shift[b,c])
  * for token t = b*N + n of x [B, N, C], r = round to x_dtype (identity for
- * fp32).  shift and scale are [B, C] in x_dtype; weight is fp32 [C].
+ * fp32).  shift and scale are per-sample rows of C values in x_dtype, row b
+ * at element offset b * mod_ld (mod_ld >= C, a multiple of 4: e.g. chunks of
+ * the shared [B, 6C] AdaLN vector); weight [C] is fp32 or w_dtype.
  * Replaces FinalLayerSharedAdaLN's norm_final + modulate
  * (local_thc.py:870-873, RMSNorm jit_shared_adaln.py:26-30, modulate
  * local_thc.py:37-38), which eager PyTorch evaluates as about eight passes
  * over the [B, N, C] tensor; here one read and one write.  C <= 2048.
  */
-int lthc_norm_modulate_fwd(const void* x, int x_dtype, const float* weight, const void* shift, const void* scale,
-                           void* y, float* inv, int64_t B, int64_t N, int64_t C, float eps, void* stream);
+int lthc_norm_modulate_fwd(const void* x, int x_dtype, const void* weight, int w_dtype, const void* shift,
+                           const void* scale, int64_t mod_ld, void* y, float* inv, int64_t B, int64_t N, int64_t C,
+                           float eps, void* stream);
 
 /*
  * Its backward, given gy = dL/dy and the forward's inv:
@@ -204,10 +207,10 @@ int lthc_norm_modulate_fwd(const void* x, int x_dtype, const float* weight, cons
  * (the fp32 gradient of the function above; reductions in a fixed order).
  */
 size_t lthc_norm_modulate_bwd_workspace_bytes(int64_t B, int64_t N, int64_t C);
-int lthc_norm_modulate_bwd(const void* gy, const void* x, int x_dtype, const float* weight, const void* scale,
-                           const float* inv, void* gx, float* gweight, float* gshift, float* gscale,
-                           int64_t B, int64_t N, int64_t C, void* workspace, size_t workspace_bytes,
-                           void* stream);
+int lthc_norm_modulate_bwd(const void* gy, const void* x, int x_dtype, const void* weight, int w_dtype,
+                           const void* scale, int64_t mod_ld, const float* inv, void* gx, float* gweight,
+                           float* gshift, float* gscale, int64_t B, int64_t N, int64_t C, void* workspace,
+                           size_t workspace_bytes, void* stream);
 
 /*
  * Q/K RMSNORM + 2-D ROPE of the branch's attention (no reference op: the
@@ -219,12 +222,13 @@ int lthc_norm_modulate_bwd(const void* gy, const void* x, int x_dtype, const flo
  *   n   = r((x * rsqrt(mean_d x^2 + eps)) * weight[d])              weight fp32 [D]
  *   out = r(r(n * r(cos[n,d])) + r(rot(n) * r(sin[n,d])))           rot(n)_{2i} = -n_{2i+1}, rot(n)_{2i+1} = n_{2i}
  * written to q_out / k_out [B, N, H, D] (x_dtype); cos / sin are fp32
- * [N, D]; r = round to x_dtype.  D must be 64; qkv, the outputs, weights
- * and tables 16-byte aligned.
+ * [N, D] (table_dtype; the table rounded to x_dtype first, as RoPE's
+ * .to(x.dtype)); weights [D] in w_dtype; w_dtype and table_dtype are fp32 or
+ * x_dtype; r = round to x_dtype.  D must be 64; every pointer 16-byte aligned.
  */
-int lthc_qk_norm_rope(const void* qkv, int x_dtype, const float* q_weight, const float* k_weight, const float* cos_table,
-                      const float* sin_table, void* q_out, void* k_out, int64_t B, int64_t N, int64_t H, int64_t D,
-                      float eps, void* stream);
+int lthc_qk_norm_rope(const void* qkv, int x_dtype, const void* q_weight, const void* k_weight, int w_dtype,
+                      const void* cos_table, const void* sin_table, int table_dtype, void* q_out, void* k_out, int64_t B,
+                      int64_t N, int64_t H, int64_t D, float eps, void* stream);
 
 /*
  * SWIGLU GATE (no reference op: SwiGLUFFN.forward's chunk + silu + mul,
@@ -243,14 +247,16 @@ int lthc_swiglu(const void* x, int x_dtype, void* out, int64_t rows, int64_t F, 
  *     RMSNorm + modulate of x as lthc_norm_modulate_fwd (y, inv); d is written
  *     to d_out.  (dz_attn, z_tmp and the second pre-norm in one pass.)
  *   lthc_gate_residual:  out = r(d + r(gate * m))   (dz_attn + gate_mlp * mlp);
- *     C % 8 == 0, every pointer 16-byte aligned.
- * All tensors in x_dtype except the fp32 weight [C] and inv [B*N] (may be NULL).
+ *     C % 8 == 0, gate_ld % 8 == 0, every pointer 16-byte aligned.
+ * Row b of a per-sample vector is at element offset b * mod_ld (gate_ld).  All
+ * tensors in x_dtype except the weight [C] (w_dtype) and inv [B*N] (fp32, may
+ * be NULL).
  */
-int lthc_gate_add_norm_modulate_fwd(const void* z, const void* a, const void* gate, int x_dtype, const float* weight,
-                                    const void* shift, const void* scale, void* d_out, void* y, float* inv, int64_t B,
-                                    int64_t N, int64_t C, float eps, void* stream);
-int lthc_gate_residual(const void* d, const void* gate, const void* m, int x_dtype, void* out, int64_t B, int64_t N,
-                       int64_t C, void* stream);
+int lthc_gate_add_norm_modulate_fwd(const void* z, const void* a, const void* gate, int x_dtype, const void* weight,
+                                    int w_dtype, const void* shift, const void* scale, int64_t mod_ld, void* d_out,
+                                    void* y, float* inv, int64_t B, int64_t N, int64_t C, float eps, void* stream);
+int lthc_gate_residual(const void* d, const void* gate, int64_t gate_ld, const void* m, int x_dtype, void* out,
+                       int64_t B, int64_t N, int64_t C, void* stream);
 
 #ifdef __cplusplus
 }

@@ -27,7 +27,7 @@ def test_library_exports_every_declared_symbol():
     for name in names:
         assert hasattr(lib, name), name
     assert sorted(_abi.EXPORTS) == names
-    assert lib.lthc_abi_version() == 2
+    assert lib.lthc_abi_version() == 3
 
 
 def _err(rc):
@@ -57,10 +57,14 @@ def test_argument_errors_are_reported_without_launching():
     assert rc == _abi.ERR_INVALID and "aligned" in msg
     rc, msg = _err(lib.lthc_weight_grad(fake, arr, _abi.F32, fake, 2, 16, 4, 768, 1, None, 0, None))
     assert rc == _abi.ERR_INVALID and "workspace" in msg
-    rc, msg = _err(lib.lthc_qk_norm_rope(fake, _abi.BF16, fake, fake, fake, fake, fake, fake, 2, 256, 12, 32, 1e-6, None))
+    rc, msg = _err(lib.lthc_qk_norm_rope(fake, _abi.BF16, fake, fake, _abi.F32, fake, fake, _abi.F32, fake, fake, 2, 256, 12, 32, 1e-6, None))
     assert rc == _abi.ERR_UNSUPPORTED and "64" in msg
-    rc, msg = _err(lib.lthc_qk_norm_rope(fake, _abi.BF16, None, fake, fake, fake, fake, fake, 2, 256, 12, 64, 1e-6, None))
+    rc, msg = _err(lib.lthc_qk_norm_rope(fake, _abi.BF16, None, fake, _abi.F32, fake, fake, _abi.F32, fake, fake, 2, 256, 12, 64, 1e-6, None))
     assert rc == _abi.ERR_INVALID and "NULL" in msg
+    rc, msg = _err(lib.lthc_norm_modulate_fwd(fake, _abi.BF16, fake, _abi.F32, fake, fake, 766, fake, None, 2, 256, 768, 1e-6, None))
+    assert rc == _abi.ERR_INVALID and "mod_ld" in msg
+    rc, msg = _err(lib.lthc_gate_residual(fake, fake, 772, fake, _abi.BF16, fake, 2, 256, 768, None))
+    assert rc == _abi.ERR_INVALID and "gate_ld" in msg
     rc, msg = _err(lib.lthc_swiglu(fake, _abi.BF16, fake, 16, 12, None))
     assert rc == _abi.ERR_UNSUPPORTED and "multiple of 8" in msg
     rc, msg = _err(lib.lthc_swiglu(ctypes.c_void_p(4096 + 8), _abi.BF16, fake, 16, 16, None))
