@@ -1,9 +1,13 @@
 """LTHC-B/4 shared-read model around the HIP interface.
 
-The workspace transformer, embedders and decoder are plain PyTorch (their
-GEMMs and attention run through hipBLASLt / the SDPA kernels of PyTorch-ROCm);
-the high-resolution interface -- shared read, lazy workspace recurrence and
-the single final materialisation -- runs through the ``jit_thc`` HIP ops.
+The high-resolution interface -- shared read, lazy workspace recurrence and
+the single final materialisation -- runs through the ``jit_thc`` HIP ops of
+:mod:`.ops`.  The workspace transformer, embedders and decoder are PyTorch
+modules whose GEMMs and attention run through hipBLASLt / the SDPA kernels of
+PyTorch-ROCm; their elementwise chains (RMSNorm + modulate, q/k norm + RoPE,
+SwiGLU, gated residuals) run through the fused HIP ops of :mod:`.ops` and
+:mod:`.ops_branch` on the GPU, with the eager sequence as the reference and
+the fallback for shapes those kernels do not take.
 
 The module tree, parameter names, initialisation and forward math follow
 flowmatching_lthc/models/local_thc.py (SharedReadLocalTHCSharedAdaLNJiT,
