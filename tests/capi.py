@@ -75,8 +75,11 @@ def gamma(alpha: torch.Tensor, betas, out_dtype=torch.float32) -> torch.Tensor:
 
 
 def recur(z: torch.Tensor, dz: torch.Tensor, gam: torch.Tensor) -> torch.Tensor:
+    return recur_into(z, dz, gam, torch.empty_like(z))
+
+
+def recur_into(z: torch.Tensor, dz: torch.Tensor, gam: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     c = z.shape[-1]
-    out = torch.empty_like(z)
     rc = _lib().lthc_recur_fwd(z.data_ptr(), dz.data_ptr(), _abi.code(z), gam.data_ptr(), _abi.code(gam), out.data_ptr(), z.numel() // c, c, _stream())
     _abi.check(rc, "lthc_recur_fwd")
     return out

@@ -196,6 +196,37 @@ def test_read_add_op_and_backward_bf16(coracle):
     assert_f32(host(w.grad), coracle.Cweight_grad(host(g), [host(z)], G)[0], tol=1e-5, what="grad w")
 
 
+@pytest.mark.parametrize("xdt", [F32, BF16, torch.float16])
+@pytest.mark.parametrize("same_gamma_dtype", [False, True])
+@pytest.mark.parametrize("C", [768, 260, 12])
+def test_recurrence_forward_both_forms(coracle, xdt, same_gamma_dtype, C):
+    """z + gamma * dz against the oracle.  16-byte aligned tensors with C a multiple of one 16-byte run take
+    the one-shot kernel; 16-bit views shifted by 4 elements (8-byte aligned) and 16-bit C = 260 or 12 take the
+    grid-stride kernel.  The two forms agree bit for bit."""
+    d = cfg(2, 16, C, 1, grads=True)
+    z, dz = dev(d["grad_z"][0] * 50.0, xdt), dev(d["dz"][0], xdt)
+    gam = dev(d["alpha"][:, 0] * 3.0)
+    if same_gamma_dtype:
+        gam = gam.to(xdt)
+    ref = coracle.Crecur(host(z), host(dz), host(gam))
+    out = capi.recur(z, dz, gam)
+    if xdt == F32:
+        assert_f32(host(out), ref, what="recurrence fp32")
+    else:
+        got, r = host(out).astype(np.float64), ref.astype(np.float64)
+        bound = 2.0**-8 * np.abs(r) + 1e-5 if xdt == BF16 else 2.0**-11 * np.abs(r) + 1e-7
+        assert (np.abs(got - r) <= bound).all(), "recurrence: more than one rounding from the exact result"
+        n = z.numel()
+        shifted = []
+        for t in (z, dz):
+            buf = torch.empty(n + 4, device=DEV, dtype=xdt)
+            buf[4:].copy_(t.reshape(-1))
+            shifted.append(buf[4:].view_as(t))
+        out_buf = torch.empty(n + 4, device=DEV, dtype=xdt)
+        alt = capi.recur_into(shifted[0], shifted[1], gam, out_buf[4:].view_as(z))
+        assert torch.equal(alt, out), "one-shot and grid-stride recurrence differ"
+
+
 def test_recurrence_backward(coracle):
     d = cfg(8, 16, 768, 2, grads=True)
     g, dz = dev(d["grad_z"][0], BF16), dev(d["dz"][0], BF16)
