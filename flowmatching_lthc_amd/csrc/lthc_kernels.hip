@@ -1648,3 +1648,5 @@ int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dty
 // Workspace accumulation of the non-shared (triangular lazy) interface.
 #include "ws_accumulate.inc"
 #include "branch_ops.inc"
+// Fused q/k RMSNorm + RoPE and attention of the branch (matrix cores).
+#include "attention.inc"

@@ -97,6 +97,18 @@ class VisionRotaryEmbeddingFast(nn.Module):
         sin = self.freqs_sin.to(x.device, x.dtype)
         return x * cos + _rotate_pairs(x) * sin
 
+    def tables(self, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+        """(cos, sin) cast to `dtype` -- the values forward() multiplies by -- converted once and kept until the
+        buffers change (a new device or dtype, or an in-place update)."""
+        if self.freqs_cos.dtype == dtype:
+            return self.freqs_cos, self.freqs_sin
+        key = (dtype, self.freqs_cos.data_ptr(), self.freqs_cos._version, self.freqs_sin.data_ptr(), self.freqs_sin._version)
+        cache = self.__dict__.get("_cast_tables")
+        if cache is None or cache[0] != key:
+            cache = (key, self.freqs_cos.to(dtype), self.freqs_sin.to(dtype))
+            self.__dict__["_cast_tables"] = cache
+        return cache[1], cache[2]
+
 
 class BottleneckPatchEmbedNHWC(nn.Module):
     """Conv patchify (in -> bottleneck, kernel = stride = patch) then 1x1 conv to C, NHWC out (local_thc.py:64-89)."""
@@ -197,6 +209,8 @@ class WorkspaceAttention(nn.Module):
         self.proj = nn.Linear(dim, dim)
         self.proj_drop = nn.Dropout(proj_drop)
         self.attn_backend = attn_backend
+        # q/k norm + RoPE + attention as one HIP pass (jit_thc::qk_norm_rope_attention) where it applies
+        self.fused_attention = True
 
     def _backends(self):
         table = {
@@ -218,12 +232,29 @@ class WorkspaceAttention(nn.Module):
             and tuple(rope.freqs_cos.shape) == (qkv.shape[1], self.head_dim)
         )
 
+    def _fused_attn(self, qkv5: torch.Tensor) -> bool:
+        """Whether jit_thc::qk_norm_rope_attention replaces the SDPA call: switched on, a fast SDPA backend
+        requested (not the math reference path), no attention dropout active, a supported shape and dtype."""
+        return (
+            self.fused_attention
+            and self.attn_backend in ("flash", "efficient")
+            and not (self.training and self.attn_drop.p > 0.0)
+            and ops_branch.attention_supported(qkv5)
+        )
+
     def forward(self, x: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> torch.Tensor:
         b, n, c = x.shape
         qkv = self.qkv(x)
         if self._fused_qk(qkv, rope):
-            # one HIP pass for q_norm + rope and k_norm + rope, with the eager sequence's roundings
             qkv5 = qkv.view(b, n, 3, self.num_heads, self.head_dim)
+            if self._fused_attn(qkv5):
+                # q/k norm + rope and the attention itself in one matrix-core pass, o as [B, N, H, D]
+                cos, sin = rope.tables(qkv.dtype)  # the values the kernel rounds the tables to, cast once
+                o = ops_branch.qk_norm_rope_attention(
+                    qkv5, self.q_norm.weight, self.k_norm.weight, cos, sin, self.q_norm.eps
+                )
+                return self.proj_drop(self.proj(o.reshape(b, n, c)))
+            # one HIP pass for q_norm + rope and k_norm + rope, with the eager sequence's roundings
             q, k = ops_branch.qk_norm_rope(
                 qkv5, self.q_norm.weight, self.k_norm.weight, rope.freqs_cos, rope.freqs_sin, self.q_norm.eps
             )

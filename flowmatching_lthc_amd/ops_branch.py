@@ -10,6 +10,9 @@ activation dtype), registered as a ``jit_thc`` custom op:
   jit_shared_adaln.py:26-30; VisionRotaryEmbeddingFast jit_shared_adaln.py:57-59),
   taking the qkv projection [B, N, 3, H, 64] and returning q and k as
   [B, N, H, 64] (the memory layout of the eager result);
+* ``jit_thc::qk_norm_rope_attention``: the same q and k followed by
+  ``F.scaled_dot_product_attention`` (local_thc.py:246-251), one matrix-core
+  pass from the qkv projection to the attention output [B, N, H, 64];
 * ``jit_thc::swiglu``: ``F.silu(x1) * x2`` of ``SwiGLUFFN.forward``
   (local_thc.py:267-269) for the w12 projection [..., 2F];
 * ``jit_thc::gate_add_norm_modulate``: ``dz_attn = gate_msa * attn``,
@@ -137,6 +140,83 @@ def _backward_qk(ctx, grad_q, grad_k):
 
 
 torch.library.register_autograd(qk_norm_rope, _backward_qk, setup_context=_setup_qk_ctx)
+
+
+# ---------------------------------------------------------------------------
+# jit_thc::qk_norm_rope_attention
+# ---------------------------------------------------------------------------
+ATTN_MAX_TOKENS = 256
+
+
+def attention_supported(qkv: Tensor) -> bool:
+    """Whether jit_thc::qk_norm_rope_attention takes qkv [B, N, 3, H, 64]: 16-bit, N a multiple of 64 up to 256."""
+    n = qkv.shape[1]
+    return (
+        qkv.is_cuda
+        and qkv.dtype in (torch.bfloat16, torch.float16)
+        and qkv.dim() == 5
+        and qkv.shape[4] == QK_HEAD_DIM
+        and n % 64 == 0
+        and 0 < n <= ATTN_MAX_TOKENS
+    )
+
+
+def qk_norm_rope_attention_eager(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, sin: Tensor, eps: float):
+    """q/k norm + RoPE, then F.scaled_dot_product_attention (default scale, no mask): o as [B, N, H, D]."""
+    q, k = qk_norm_rope_eager(qkv, q_weight, k_weight, cos, sin, eps)
+    v = qkv[:, :, 2]
+    # [B, H, N, D] operands made contiguous (no transposed views in the batched products)
+    q, k, v = (t.transpose(1, 2).contiguous() for t in (q, k, v))
+    o = F.scaled_dot_product_attention(q, k, v)
+    return o.transpose(1, 2)
+
+
+@torch.library.custom_op("jit_thc::qk_norm_rope_attention", mutates_args=())
+def qk_norm_rope_attention(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, sin: Tensor, eps: float) -> Tensor:
+    """softmax(q_n k_n^T / sqrt(64)) v for q_n, k_n = qk_norm_rope(...): o as [B, N, H, 64] in qkv's dtype (bf16 or
+    fp16, N a multiple of 64 up to 256), one pass over qkv on the matrix cores."""
+    _on_gpu(qkv, q_weight, k_weight, cos, sin)
+    b, n, h = _check_qk(qkv, q_weight, k_weight, cos, sin)
+    if not attention_supported(qkv):
+        raise ValueError(f"qkv must be bf16 or fp16 [B,N,3,H,64] with N a multiple of 64 up to {ATTN_MAX_TOKENS}, got "
+                         f"{tuple(qkv.shape)} {qkv.dtype}")
+    qkv = _aligned(qkv)
+    qw, kw, c, s = (t if t.dtype == qkv.dtype else t.float() for t in (q_weight, k_weight, cos, sin))
+    if kw.dtype != qw.dtype:
+        qw, kw = qw.float(), kw.float()
+    if s.dtype != c.dtype:
+        c, s = c.float(), s.float()
+    qw, kw, c, s = (_aligned(t) for t in (qw, kw, c, s))
+    out = torch.empty((b, n, h, QK_HEAD_DIM), device=qkv.device, dtype=qkv.dtype)
+    with _on_device(qkv):
+        rc = _abi.load().lthc_qk_norm_rope_attention(
+            qkv.data_ptr(), _abi.code(qkv), qw.data_ptr(), kw.data_ptr(), _abi.code(qw), c.data_ptr(), s.data_ptr(),
+            _abi.code(c), out.data_ptr(), b, n, h, QK_HEAD_DIM, eps, QK_HEAD_DIM**-0.5, _abi.stream_of(qkv),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_qk_norm_rope_attention")
+    return out
+
+
+@qk_norm_rope_attention.register_fake
+def _(qkv, q_weight, k_weight, cos, sin, eps):
+    b, n, _, h, d = qkv.shape
+    return qkv.new_empty((b, n, h, d))
+
+
+def _backward_qk_attention(ctx, grad):
+    qkv, q_weight, k_weight, cos, sin = ctx.saved_tensors
+    need = ctx.needs_input_grad
+    with torch.enable_grad():
+        leaves = [t.detach().requires_grad_(bool(r)) for t, r in zip((qkv, q_weight, k_weight), need[:3])]
+        o = qk_norm_rope_attention_eager(leaves[0], leaves[1], leaves[2], cos, sin, ctx.eps)
+        wanted = [t for t in leaves if t.requires_grad]
+        got = torch.autograd.grad([o], wanted, [grad], allow_unused=True) if wanted else []
+    it = iter(got)
+    res = [next(it) if t.requires_grad else None for t in leaves]
+    return res[0], res[1], res[2], None, None, None
+
+
+torch.library.register_autograd(qk_norm_rope_attention, _backward_qk_attention, setup_context=_setup_qk_ctx)
 
 
 # ---------------------------------------------------------------------------

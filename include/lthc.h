@@ -231,6 +231,24 @@ int lthc_qk_norm_rope(const void* qkv, int x_dtype, const void* q_weight, const 
                       int64_t N, int64_t H, int64_t D, float eps, void* stream);
 
 /*
+ * Q/K RMSNORM + ROPE FUSED WITH THE ATTENTION (no reference op: the reference
+ * evaluates WorkspaceAttention.forward, local_thc.py:246-251, as the q/k
+ * norms, RoPE and F.scaled_dot_product_attention).  For qkv [B, N, 3, H, D]:
+ *   q_n, k_n = the normalised q and k of lthc_qk_norm_rope (bit-identical)
+ *   out[b, n, h, :] = sum_m softmax_m(scale * q_n . k_m) v[b, m, h, :]
+ * written as [B, N, H, D] (x_dtype, the [B, N, C] layout of the output
+ * projection's input).  Scores, softmax and the output accumulate in fp32;
+ * the probabilities are rounded to x_dtype before they multiply V (as flash
+ * attention does) and the output is divided by the fp32 row sum and rounded
+ * once.  x_dtype bf16 or fp16; D == 64; N a multiple of 64, at most 256;
+ * scale > 0 (F.scaled_dot_product_attention's default is 1 / sqrt(D));
+ * weights, tables and alignment as lthc_qk_norm_rope.  No dropout.
+ */
+int lthc_qk_norm_rope_attention(const void* qkv, int x_dtype, const void* q_weight, const void* k_weight, int w_dtype,
+                                const void* cos_table, const void* sin_table, int table_dtype, void* out, int64_t B,
+                                int64_t N, int64_t H, int64_t D, float eps, float scale, void* stream);
+
+/*
  * SWIGLU GATE (no reference op: SwiGLUFFN.forward's chunk + silu + mul,
  * local_thc.py:267-269, three eager passes):
  *   out[r, f] = r(r(a / (1 + exp(-a))) * v),  a = x[r, f], v = x[r, F + f]

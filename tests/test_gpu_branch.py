@@ -1,5 +1,5 @@
-"""GPU parity of the fused branch ops (jit_thc::qk_norm_rope, jit_thc::swiglu) against the eager sequences
-they replace (MI355X only).
+"""GPU parity of the fused branch ops (jit_thc::qk_norm_rope, jit_thc::qk_norm_rope_attention, jit_thc::swiglu,
+the gated residuals) against the eager sequences they replace (MI355X only).
 
 The eager sequences are the model's own modules (RMSNorm, VisionRotaryEmbeddingFast on the permuted q/k
 views of the projection; chunk + F.silu + mul), so the check covers the exact op chain the kernels stand in
@@ -198,3 +198,118 @@ def test_gated_residual_ops_match_eager(dtype):
         assert err <= (1e-5 if dtype == torch.float32 else 2e-2), f"grad {name}: {err:.3e}"
     err = ((wl.grad - we.grad).abs().max() / we.grad.abs().max()).item()
     assert err <= 1e-4, f"grad weight: {err:.3e}"
+
+
+# ---------------------------------------------------------------------------
+# jit_thc::qk_norm_rope_attention
+# ---------------------------------------------------------------------------
+def attention_exact(q, k, v):
+    """softmax(q k^T / sqrt(64)) v in float64 on the CPU; q, k, v and the result [B, N, H, 64]."""
+    q, k, v = (t.detach().double().cpu().transpose(1, 2) for t in (q, k, v))
+    s = q @ k.transpose(-1, -2).contiguous() / 8.0
+    return (torch.softmax(s, dim=-1) @ v).transpose(1, 2)
+
+
+def random_rope_tables(n, gen):
+    theta = torch.rand((n, 64), generator=gen) * 6.2831853
+    return torch.cos(theta).to(DEV), torch.sin(theta).to(DEV)
+
+
+@pytest.mark.parametrize("dtype,N,H", [(torch.bfloat16, 256, 12), (torch.float16, 256, 4), (torch.bfloat16, 64, 3),
+                                       (torch.bfloat16, 192, 2)])
+def test_qk_norm_rope_attention_matches_exact(dtype, N, H):
+    """Against softmax attention in float64 on the op's own normalised q and k (qk_norm_rope, which the kernel
+    reproduces bit for bit) and v: every element within one rounding of the probabilities and one of the output,
+    |d| <= u (max|v| + |ref|) with u = 2^-8 (bf16) or 2^-11 (fp16), and no further from the exact result than
+    torch's scaled_dot_product_attention on the same q, k, v."""
+    print(f"case dtype={dtype} N={N} H={H}", flush=True)
+    B = 2
+    gen = torch.Generator().manual_seed(7)
+    qkv = (torch.randn((B, N, 3, H, 64), generator=gen) * 2.0).to(DEV, dtype)
+    qw = (torch.randn(64, generator=gen) * 0.2 + 1).to(DEV)
+    kw = (torch.randn(64, generator=gen) * 0.2 + 1).to(DEV)
+    cos, sin = random_rope_tables(N, gen)
+    o = OB.qk_norm_rope_attention(qkv, qw, kw, cos, sin, 1e-6)
+    assert o.shape == (B, N, H, 64) and o.dtype == dtype and o.is_contiguous()
+    q, k = OB.qk_norm_rope(qkv, qw, kw, cos, sin, 1e-6)
+    v = qkv[:, :, 2]
+    ref = attention_exact(q, k, v)
+    d = (o.double().cpu() - ref).abs()
+    u = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11
+    vmax = v.double().abs().max().item()
+    bad = (d > u * (vmax + ref.abs())).sum().item()
+    assert bad == 0, f"{bad} elements beyond one rounding (max |d| {d.max().item():.3e})"
+    sdpa = torch.nn.functional.scaled_dot_product_attention(*(t.transpose(1, 2).contiguous() for t in (q, k, v)))
+    e_sdpa = (sdpa.transpose(1, 2).double().cpu() - ref).abs().max().item()
+    assert d.max().item() <= max(1.5 * e_sdpa, u * vmax), (d.max().item(), e_sdpa)
+    # the op's eager restatement is the path it replaces
+    eager = OB.qk_norm_rope_attention_eager(qkv, qw, kw, cos, sin, 1e-6)
+    assert (eager.double().cpu() - ref).abs().max().item() <= max(2 * e_sdpa, u * vmax)
+
+
+def test_qk_norm_rope_attention_gradients_and_errors():
+    """The backward (recomputed through the eager sequence) matches autograd of that sequence; unsupported
+    shapes and dtypes raise ValueError."""
+    print("case attention gradients", flush=True)
+    B, N, H = 2, 256, 4
+    gen = torch.Generator().manual_seed(8)
+    qkv = (torch.randn((B, N, 3, H, 64), generator=gen) * 2.0).to(DEV, torch.bfloat16)
+    w0 = (torch.randn(64, generator=gen) * 0.2 + 1).to(DEV)
+    w1 = (torch.randn(64, generator=gen) * 0.2 + 1).to(DEV)
+    cos, sin = random_rope_tables(N, gen)
+    g = (torch.randn((B, N, H, 64), generator=gen) * 0.1).to(DEV, torch.bfloat16)
+    grads = []
+    for fn in (OB.qk_norm_rope_attention, OB.qk_norm_rope_attention_eager):
+        leaves = [t.clone().requires_grad_() for t in (qkv, w0, w1)]
+        fn(*leaves, cos, sin, 1e-6).backward(g)
+        grads.append([t.grad.double() for t in leaves])
+    for name, a, b in zip(("qkv", "q_weight", "k_weight"), *grads):
+        err = ((a - b).abs().max() / b.abs().max()).item()
+        assert err <= 1e-2, f"grad {name}: {err:.3e}"
+    with pytest.raises(ValueError):
+        OB.qk_norm_rope_attention(qkv[:, :100], w0, w1, cos[:100], sin[:100], 1e-6)
+    with pytest.raises(ValueError):
+        OB.qk_norm_rope_attention(qkv.float(), w0, w1, cos, sin, 1e-6)
+
+
+def test_model_fused_attention_matches_sdpa_bf16():
+    """A model with 64-wide heads over an 8x8 workspace (N = 64) under bf16 autocast: the fused attention path
+    stays as close to the fp32 result as the SDPA path does, and the math backend keeps SDPA."""
+    cfg = dict(input_size=128, patch_size=4, hidden_size=192, depth=2, num_heads=3, num_classes=10,
+               bottleneck_dim=16, workspace_grid=8)
+    m = M.randomize_parameters(M.SharedReadLocalTHCSharedAdaLNJiT(**cfg), seed=5).to(DEV).eval()
+    gen = torch.Generator().manual_seed(9)
+    x = torch.randn((2, 3, 128, 128), generator=gen).to(DEV)
+    t = torch.rand((2,), generator=gen).to(DEV)
+    y = torch.randint(0, 10, (2,), generator=gen).to(DEV)
+    calls = {"n": 0}
+    real = OB.qk_norm_rope_attention
+
+    def count(*a):
+        calls["n"] += 1
+        return real(*a)
+
+    attns = [blk.branch.attn for blk in m.blocks]
+    with torch.no_grad():
+        exact = m(x, t, y).double()
+        outs = {}
+        for fused in (True, False):
+            for a in attns:
+                a.fused_attention = fused
+            OB.qk_norm_rope_attention = count
+            try:
+                with torch.autocast("cuda", dtype=torch.bfloat16):
+                    outs[fused] = m(x, t, y).double()
+            finally:
+                OB.qk_norm_rope_attention = real
+        assert calls["n"] == 2, calls
+        for a in attns:
+            a.fused_attention, a.attn_backend = True, "math"
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            m(x, t, y)
+        assert calls["n"] == 2, "the math backend must keep SDPA"
+
+    def rel(a):
+        return ((a - exact).abs().max() / exact.abs().max()).item()
+
+    assert rel(outs[True]) <= max(1.5 * rel(outs[False]), 1e-3), (rel(outs[True]), rel(outs[False]))
