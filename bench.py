@@ -445,7 +445,8 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
 
     def forward():
         x0v, z = ops.read_with_residual(x0, alpha.to(bf16))  # as the model's forward_lazy
-        gam = ops.lazy_gamma_stack(alpha.to(bf16), torch.stack([b.to(bf16) for b in betas]))
+        # gamma rows as one unbind (its backward is one stack, not a zero-fill + copy + add per layer)
+        gam = ops.lazy_gamma_stack(alpha.to(bf16), torch.stack([b.to(bf16) for b in betas])).unbind(0)
         zs, dzv = [z], []
         for l in range(L):
             z, d = ops.lazy_workspace_step(z, dzs[l], gam[l])  # as the model's forward_lazy

@@ -43,6 +43,7 @@ EXPORTS = (
     "lthc_norm_modulate_bwd",
     "lthc_qk_norm_rope",
     "lthc_qk_norm_rope_attention",
+    "lthc_decoder_fwd",
     "lthc_swiglu",
     "lthc_gate_add_norm_modulate_fwd",
     "lthc_gate_residual",
@@ -86,6 +87,9 @@ def load() -> ctypes.CDLL:
         "lthc_qk_norm_rope": [vp, ci, vp, vp, ci, vp, vp, ci, vp, vp, i64, i64, i64, i64, ctypes.c_float, vp],
         "lthc_qk_norm_rope_attention": [
             vp, ci, vp, vp, ci, vp, vp, ci, vp, i64, i64, i64, i64, ctypes.c_float, ctypes.c_float, vp,
+        ],  # fmt: skip
+        "lthc_decoder_fwd": [
+            vp, ci, vp, ci, vp, vp, i64, vp, ci, vp, ci, vp, i64, i64, i64, i64, i64, i64, ctypes.c_float, vp,
         ],  # fmt: skip
         "lthc_swiglu": [vp, ci, vp, i64, i64, vp],
         "lthc_gate_add_norm_modulate_fwd": [

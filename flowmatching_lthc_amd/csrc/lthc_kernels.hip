@@ -1650,3 +1650,5 @@ int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dty
 #include "branch_ops.inc"
 // Fused q/k RMSNorm + RoPE and attention of the branch (matrix cores).
 #include "attention.inc"
+// The decoder head (norm + modulate + linear + unpatchify) on the matrix cores.
+#include "decoder.inc"

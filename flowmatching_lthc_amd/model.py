@@ -467,6 +467,8 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
         self.initialize_weights()
         self.shared_read = SharedLocalRead(high_grid, workspace_grid, hidden_size, self.pool_groups, use_softmax_write=True)
         self.use_lazy = bool(use_lazy)
+        # decoder head as one HIP pass (jit_thc::decoder_head) where it applies
+        self.fused_decoder = True
 
     # -- initialisation (local_thc.py:944-970, :1004-1007) ------------------------------------------
     def initialize_weights(self) -> None:
@@ -519,7 +521,22 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
 
     def _decode(self, x_hi: torch.Tensor, t2: torch.Tensor) -> torch.Tensor:
         b, hh, wh, c_dim = x_hi.shape
-        return self.unpatchify(self.final_layer(x_hi.reshape(b, hh * wh, c_dim), t2))
+        x = x_hi.reshape(b, hh * wh, c_dim)
+        fl = self.final_layer
+        if (
+            self.fused_decoder
+            and t2.dtype == x.dtype
+            and isinstance(fl.norm_final, RMSNorm)
+            and fl.linear.bias is not None
+            and ops.decoder_head_supported(x, fl.linear.weight)
+        ):
+            # RMSNorm + modulate + linear + unpatchify in one pass (jit_thc::decoder_head): y never reaches memory
+            shift, scale = t2.chunk(2, dim=1)
+            return ops.decoder_head(
+                x, fl.norm_final.weight, shift, scale, fl.linear.weight, fl.linear.bias, fl.norm_final.eps, hh,
+                self.patch_size,
+            )
+        return self.unpatchify(fl(x, t2))
 
     def forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         t6, t2 = self._conditioning(t, y)

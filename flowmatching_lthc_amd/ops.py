@@ -1000,6 +1000,112 @@ def _backward_norm(ctx, grad_y, grad_inv):
 torch.library.register_autograd(norm_modulate, _backward_norm, setup_context=_setup_norm_ctx)
 
 
+# ---------------------------------------------------------------------------
+# DECODER HEAD: RMSNorm + modulate + linear + unpatchify in one pass (no reference op:
+# FinalLayerSharedAdaLN.forward and unpatchify, local_thc.py:865-873 and :972-980, are eager torch)
+# ---------------------------------------------------------------------------
+DECODER_OUTPUTS = 48
+DECODER_MAX_CHANNELS = 768
+
+
+def decoder_head_supported(x: Tensor, lin_weight: Tensor) -> bool:
+    """Whether jit_thc::decoder_head takes x [B, T, C]: 16-bit, C a multiple of 32 up to 768, T a multiple of 64,
+    48 outputs per token."""
+    return (
+        x.is_cuda
+        and x.dim() == 3
+        and x.dtype in (torch.bfloat16, torch.float16)
+        and x.shape[2] % 32 == 0
+        and x.shape[2] <= DECODER_MAX_CHANNELS
+        and x.shape[1] % 64 == 0
+        and tuple(lin_weight.shape) == (DECODER_OUTPUTS, x.shape[2])
+    )
+
+
+def decoder_head_eager(x, norm_weight, shift, scale, lin_weight, lin_bias, eps: float, h: int, patch: int) -> Tensor:
+    """The eager sequence: modulate(RMSNorm(x)) in x.dtype, the linear layer with its weight and bias cast to
+    x.dtype (as autocast casts them), then unpatchify [B, h*w, P*P*CO] -> [B, CO, h*P, w*P]."""
+    xf = x.float()
+    n = (xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps) * norm_weight).to(x.dtype)
+    y = n * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1)
+    o = torch.nn.functional.linear(y, lin_weight.to(x.dtype), lin_bias.to(x.dtype))
+    b, t, _ = x.shape
+    w = t // h
+    co = o.shape[-1] // (patch * patch)
+    o = o.reshape(b, h, w, patch, patch, co).permute(0, 5, 1, 3, 2, 4)
+    return o.reshape(b, co, h * patch, w * patch)
+
+
+@torch.library.custom_op("jit_thc::decoder_head", mutates_args=())
+def decoder_head(
+    x: Tensor, norm_weight: Tensor, shift: Tensor, scale: Tensor, lin_weight: Tensor, lin_bias: Tensor, eps: float,
+    h: int, patch: int,
+) -> Tensor:
+    """unpatchify(Linear(modulate(RMSNorm(x), shift, scale))) for x [B, h*w, C] (bf16 / fp16): the image
+    [B, CO, h*P, w*P] in x.dtype, one pass over x (y stays in registers; the 48-output product on the matrix
+    cores)."""
+    _on_gpu(x, norm_weight, shift, scale, lin_weight, lin_bias)
+    if not decoder_head_supported(x, lin_weight):
+        raise ValueError(
+            f"x must be bf16 or fp16 [B, T, C] with T % 64 == 0, C % 32 == 0, C <= {DECODER_MAX_CHANNELS} and "
+            f"lin_weight [{DECODER_OUTPUTS}, C]; got {tuple(x.shape)} {x.dtype}, {tuple(lin_weight.shape)}"
+        )
+    b, t, c = x.shape
+    if h <= 0 or t % h != 0 or patch <= 0 or DECODER_OUTPUTS % (patch * patch) != 0:
+        raise ValueError(f"token grid {h} x {t // max(h, 1)} and patch {patch} do not fit {t} tokens, 48 outputs")
+    w = t // h
+    co = DECODER_OUTPUTS // (patch * patch)
+    for name, v in (("shift", shift), ("scale", scale)):
+        if tuple(v.shape) != (b, c) or v.dtype != x.dtype:
+            raise ValueError(f"{name} must be [{b}, {c}] {x.dtype}, got {tuple(v.shape)} {v.dtype}")
+    if tuple(norm_weight.shape) != (c,) or tuple(lin_bias.shape) != (DECODER_OUTPUTS,):
+        raise ValueError(f"norm_weight [{c}] and lin_bias [{DECODER_OUTPUTS}] expected")
+    x = _prep(x)
+    (shift, scale), ld = _mod_rows(shift, scale, elems=1)
+    nw = _norm_weight(norm_weight)
+    lw = lin_weight if lin_weight.dtype in (torch.float32, x.dtype) else lin_weight.float()
+    lb = lin_bias if lin_bias.dtype in (torch.float32, x.dtype) else lin_bias.float()
+    lw, lb = lw.contiguous(), lb.contiguous()
+    if lw.data_ptr() % 16 != 0:
+        lw = lw.clone()
+    img = torch.empty((b, co, h * patch, w * patch), device=x.device, dtype=x.dtype)
+    with _on_device(x):
+        rc = _abi.load().lthc_decoder_fwd(
+            x.data_ptr(), _abi.code(x), nw.data_ptr(), _abi.code(nw), shift.data_ptr(), scale.data_ptr(), ld,
+            lw.data_ptr(), _abi.code(lw), lb.data_ptr(), _abi.code(lb), img.data_ptr(), b, h, w, c, patch, co, eps,
+            _abi.stream_of(x),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_decoder_fwd")
+    return img
+
+
+@decoder_head.register_fake
+def _(x, norm_weight, shift, scale, lin_weight, lin_bias, eps, h, patch):
+    b, t, _ = x.shape
+    co = DECODER_OUTPUTS // (patch * patch)
+    return x.new_empty((b, co, h * patch, (t // h) * patch))
+
+
+def _setup_decoder_ctx(ctx, inputs, output):
+    ctx.save_for_backward(*inputs[:6])
+    ctx.geom = inputs[6:]
+
+
+def _backward_decoder(ctx, grad):
+    saved = ctx.saved_tensors
+    need = ctx.needs_input_grad[:6]
+    with torch.enable_grad():
+        leaves = [t.detach().requires_grad_(bool(r)) for t, r in zip(saved, need)]
+        out = decoder_head_eager(*leaves, *ctx.geom)
+        wanted = [t for t in leaves if t.requires_grad]
+        got = torch.autograd.grad([out], wanted, [grad], allow_unused=True) if wanted else []
+    it = iter(got)
+    return (*[next(it) if t.requires_grad else None for t in leaves], None, None, None)
+
+
+torch.library.register_autograd(decoder_head, _backward_decoder, setup_context=_setup_decoder_ctx)
+
+
 # Reference-style aliases (local_thc_triton_kernels.py exports these names).
 triton_final_accumulate_b4_traceable = final_accumulate_b4_traceable
 triton_final_accumulate_b4_12_traceable = final_accumulate_b4_12_traceable

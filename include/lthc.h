@@ -249,6 +249,25 @@ int lthc_qk_norm_rope_attention(const void* qkv, int x_dtype, const void* q_weig
                                 int64_t N, int64_t H, int64_t D, float eps, float scale, void* stream);
 
 /*
+ * DECODER HEAD (no reference op: FinalLayerSharedAdaLN.forward and
+ * unpatchify, local_thc.py:865-873 and :972-980, are eager torch).  For the
+ * materialised x [B, h*w, C] (x_dtype bf16 or fp16):
+ *   y   = RMSNorm + modulate of x as lthc_norm_modulate_fwd (the same roundings)
+ *   o   = r(sum_c y[t,c] * r(W[j,c]) + r(bias[j]))        j < 48 = P*P*CO
+ *   img[b, ci, hp*P + p1, wp*P + p2] = o[hp*w + wp, (p1*P + p2)*CO + ci]
+ * written to img [B, CO, h*P, w*P] (x_dtype).  The product accumulates in
+ * fp32 (matrix cores); W and bias are rounded to x_dtype first, as autocast
+ * casts them.  norm_weight [C], lin_weight [48, C] and lin_bias [48] are fp32
+ * or x_dtype; shift / scale rows [B, C] at row stride mod_ld, x_dtype.
+ * C a multiple of 32 up to 768; h*w a multiple of 64; x and lin_weight
+ * 16-byte aligned.
+ */
+int lthc_decoder_fwd(const void* x, int x_dtype, const void* norm_weight, int nw_dtype, const void* shift,
+                     const void* scale, int64_t mod_ld, const void* lin_weight, int lw_dtype, const void* lin_bias,
+                     int lb_dtype, void* img, int64_t B, int64_t h, int64_t w, int64_t C, int64_t P, int64_t CO,
+                     float eps, void* stream);
+
+/*
  * SWIGLU GATE (no reference op: SwiGLUFFN.forward's chunk + silu + mul,
  * local_thc.py:267-269, three eager passes):
  *   out[r, f] = r(r(a / (1 + exp(-a))) * v),  a = x[r, f], v = x[r, F + f]

@@ -313,3 +313,95 @@ def test_model_fused_attention_matches_sdpa_bf16():
         return ((a - exact).abs().max() / exact.abs().max()).item()
 
     assert rel(outs[True]) <= max(1.5 * rel(outs[False]), 1e-3), (rel(outs[True]), rel(outs[False]))
+
+
+# ---------------------------------------------------------------------------
+# jit_thc::decoder_head (RMSNorm + modulate + linear + unpatchify)
+# ---------------------------------------------------------------------------
+def unpatchify(o, h, p=4, co=3):
+    b, t, _ = o.shape
+    w = t // h
+    return o.reshape(b, h, w, p, p, co).permute(0, 5, 1, 3, 2, 4).reshape(b, co, h * p, w * p)
+
+
+@pytest.mark.parametrize("dtype,pdt,C,h", [(torch.bfloat16, torch.float32, 768, 64), (torch.bfloat16, torch.bfloat16, 768, 16),
+                                           (torch.float16, torch.float32, 192, 8)])
+def test_decoder_head_matches_exact(dtype, pdt, C, h):
+    """Against y W^T + b in float64, y being the norm_modulate op's output (the kernel's rounding sequence) and W, b
+    rounded to the activation dtype: each pixel within one output rounding plus two ulps of every y element (a
+    different reduction order for the inverse RMS can move a y rounding):
+    |d| <= u |o| + 4u sum_c |y_c W_jc|,  u = 2^-8 (bf16) or 2^-11 (fp16)."""
+    from flowmatching_lthc_amd import ops
+
+    print(f"case dtype={dtype} params={pdt} C={C} h={h}", flush=True)
+    B, T = 2, h * h
+    gen = torch.Generator().manual_seed(11)
+    x = (torch.randn((B, T, C), generator=gen) * 2.0).to(DEV, dtype)
+    t2 = (torch.randn((B, 2 * C), generator=gen) * 0.3).to(DEV, dtype)
+    shift, scale = t2.chunk(2, dim=1)
+    nw = (torch.randn(C, generator=gen) * 0.2 + 1).to(DEV, pdt)
+    lw = (torch.randn((48, C), generator=gen) * 0.05).to(DEV, pdt)
+    lb = (torch.randn(48, generator=gen) * 0.1).to(DEV, pdt)
+    img = ops.decoder_head(x, nw, shift, scale, lw, lb, 1e-6, h, 4)
+    assert img.shape == (B, 3, 4 * h, 4 * h) and img.dtype == dtype
+    y = ops.norm_modulate(x, nw, shift, scale, 1e-6)[0].double().cpu()
+    W, bb = lw.to(dtype).double().cpu(), lb.to(dtype).double().cpu()
+    o = y @ W.T + bb
+    mag = y.abs() @ W.abs().T
+    u = 2.0**-8 if dtype == torch.bfloat16 else 2.0**-11
+    ref, bound = unpatchify(o, h), unpatchify(u * o.abs() + 4 * u * mag, h)
+    d = (img.double().cpu() - ref).abs()
+    assert (d <= bound).all(), f"max excess {(d - bound).max().item():.3e}"
+    eager = ops.decoder_head_eager(x, nw, shift, scale, lw, lb, 1e-6, h, 4)
+    assert ((eager.double().cpu() - ref).abs() <= bound).all(), "the eager restatement is the same function"
+    with pytest.raises(ValueError):
+        ops.decoder_head(x.float(), nw, shift.float(), scale.float(), lw, lb, 1e-6, h, 4)
+
+
+def test_decoder_head_gradients():
+    """The backward (recomputed through the eager sequence) gives the eager sequence's gradients."""
+    from flowmatching_lthc_amd import ops
+
+    print("case decoder gradients", flush=True)
+    B, C, h = 2, 192, 8
+    gen = torch.Generator().manual_seed(12)
+    x = (torch.randn((B, h * h, C), generator=gen) * 2.0).to(DEV, torch.bfloat16)
+    t2 = (torch.randn((B, 2 * C), generator=gen) * 0.3).to(DEV, torch.bfloat16)
+    nw = (torch.randn(C, generator=gen) * 0.2 + 1).to(DEV)
+    lw = (torch.randn((48, C), generator=gen) * 0.05).to(DEV)
+    lb = (torch.randn(48, generator=gen) * 0.1).to(DEV)
+    g = torch.randn((B, 3, 4 * h, 4 * h), generator=gen).to(DEV, torch.bfloat16)
+    grads = []
+    for fn in (ops.decoder_head, ops.decoder_head_eager):
+        xl, tl = x.clone().requires_grad_(), t2.clone().requires_grad_()
+        ws = [t.clone().requires_grad_() for t in (nw, lw, lb)]
+        sh, sc = tl.chunk(2, dim=1)
+        fn(xl, ws[0], sh, sc, ws[1], ws[2], 1e-6, h, 4).backward(g)
+        grads.append([xl.grad.double(), tl.grad.double()] + [w.grad.double() for w in ws])
+    for name, a, b in zip(("x", "t2", "norm_weight", "lin_weight", "lin_bias"), *grads):
+        err = ((a - b).abs().max() / b.abs().max()).item()
+        assert err <= 1e-3, f"grad {name}: {err:.3e}"
+
+
+def test_model_fused_decoder_matches_unfused_bf16():
+    """Under bf16 autocast the fused decoder head stays as close to the fp32 model as the unfused head does."""
+    cfg = dict(input_size=128, patch_size=4, hidden_size=192, depth=2, num_heads=3, num_classes=10,
+               bottleneck_dim=16, workspace_grid=8)
+    m = M.randomize_parameters(M.SharedReadLocalTHCSharedAdaLNJiT(**cfg), seed=6).to(DEV).eval()
+    gen = torch.Generator().manual_seed(13)
+    x = torch.randn((2, 3, 128, 128), generator=gen).to(DEV)
+    t = torch.rand((2,), generator=gen).to(DEV)
+    y = torch.randint(0, 10, (2,), generator=gen).to(DEV)
+    with torch.no_grad():
+        exact = m(x, t, y).double()
+        outs = {}
+        for fused in (True, False):
+            m.fused_decoder = fused
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                outs[fused] = m(x, t, y).double()
+
+    def rel(a, b=exact):
+        return ((a - b).abs().max() / b.abs().max()).item()
+
+    assert rel(outs[True], outs[False]) <= 2e-2, rel(outs[True], outs[False])
+    assert rel(outs[True]) <= max(1.5 * rel(outs[False]), 1e-3), (rel(outs[True]), rel(outs[False]))

@@ -60,8 +60,9 @@ def test_b4_bf16_autocast_is_no_worse_than_torch_eager():
     torch.manual_seed(0)
     ours = M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=3).to(DEV).eval()
     ref = conv_interface(M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=3), "reshape").to(DEV).eval()
-    for blk in ref.blocks:  # the torch reference keeps torch's attention (SDPA)
+    for blk in ref.blocks:  # the torch reference keeps torch's attention (SDPA) and decoder head
         blk.branch.attn.fused_attention = False
+    ref.fused_decoder = False
     gen = torch.Generator().manual_seed(4)
     x = torch.randn(4, 3, 256, 256, generator=gen).to(DEV)
     t = torch.rand(4, generator=gen).to(DEV)
