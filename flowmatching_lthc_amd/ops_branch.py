@@ -20,9 +20,10 @@ activation dtype), registered as a ``jit_thc`` custom op:
   ``WorkspaceSharedAdaLNBranch.forward`` (local_thc.py:319-322);
 * ``jit_thc::gate_residual``: its ``dz_attn + gate_mlp * mlp`` (:322-323).
 
-The backward of the first three recomputes the eager sequence under autograd
-(the forward's values are those of that sequence), so training through them
-matches the eager model's gradients; gate_residual's is its closed form.
+The backward of all but gate_residual recomputes the eager sequence under
+autograd (the forward's values are those of that sequence; the attention's
+products accumulate in fp32 as SDPA's do), so training through them matches
+the eager model's gradients; gate_residual's is its closed form.
 """
 
 from __future__ import annotations
