@@ -924,7 +924,8 @@ def _mod_rows(*ts: Tensor, elems: int = 4) -> tuple[list[Tensor], int]:
 def _norm_weight(weight: Tensor) -> Tensor:
     """The RMSNorm weight as passed to the kernels: fp32, bf16 or fp16, contiguous."""
     w = weight if weight.dtype in (torch.float32, torch.bfloat16, torch.float16) else weight.float()
-    return w.contiguous()
+    w = w.contiguous()
+    return w if w.data_ptr() % (4 * w.element_size()) == 0 else w.clone()  # 4-element vector loads
 
 
 @torch.library.custom_op("jit_thc::norm_modulate", mutates_args=())

@@ -191,7 +191,8 @@ int lthc_ws_accumulate_bwd(const void* g, const void* const* dz, int x_dtype, co
  * for token t = b*N + n of x [B, N, C], r = round to x_dtype (identity for
  * fp32).  shift and scale are per-sample rows of C values in x_dtype, row b
  * at element offset b * mod_ld (mod_ld >= C, a multiple of 4: e.g. chunks of
- * the shared [B, 6C] AdaLN vector); weight [C] is fp32 or w_dtype.
+ * the shared [B, 6C] AdaLN vector); weight [C] is fp32 or w_dtype, aligned
+ * to 4 elements.
  * Replaces FinalLayerSharedAdaLN's norm_final + modulate
  * (local_thc.py:870-873, RMSNorm jit_shared_adaln.py:26-30, modulate
  * local_thc.py:37-38), which eager PyTorch evaluates as about eight passes
