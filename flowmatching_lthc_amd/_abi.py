@@ -44,6 +44,7 @@ EXPORTS = (
     "lthc_qk_norm_rope",
     "lthc_qk_norm_rope_attention",
     "lthc_decoder_fwd",
+    "lthc_cast_many",
     "lthc_swiglu",
     "lthc_gate_add_norm_modulate_fwd",
     "lthc_gate_residual",
@@ -91,6 +92,7 @@ def load() -> ctypes.CDLL:
         "lthc_decoder_fwd": [
             vp, ci, vp, ci, vp, vp, i64, vp, ci, vp, ci, vp, i64, i64, i64, i64, i64, i64, ctypes.c_float, vp,
         ],  # fmt: skip
+        "lthc_cast_many": [vp, vp, i64, vp, ci, vp],
         "lthc_swiglu": [vp, ci, vp, i64, i64, vp],
         "lthc_gate_add_norm_modulate_fwd": [
             vp, vp, vp, ci, vp, ci, vp, vp, i64, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp,

@@ -1652,3 +1652,5 @@ int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dty
 #include "attention.inc"
 // The decoder head (norm + modulate + linear + unpatchify) on the matrix cores.
 #include "decoder.inc"
+// One-launch dtype conversion of many weights (autocast's per-forward casts).
+#include "cast_many.inc"

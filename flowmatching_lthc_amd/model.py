@@ -21,7 +21,7 @@ from __future__ import annotations
 
 import math
 import re
-from contextlib import nullcontext
+from contextlib import contextmanager, nullcontext
 
 import torch
 import torch.nn as nn
@@ -35,6 +35,18 @@ from .local_thc import LayerLocalWrite, SharedLocalRead
 def modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """x * (1 + scale) + shift with per-sample [B, C] shift/scale (local_thc.py:37-38)."""
     return x * (1 + scale.unsqueeze(1)) + shift.unsqueeze(1)
+
+
+class CastLinear(nn.Linear):
+    """nn.Linear that, while the model's forward has converted every weight in one batched launch
+    (``SharedReadLocalTHCSharedAdaLNJiT._converted_weights``), multiplies by that (weight, bias) pair: the values
+    autocast's own per-layer conversion would give.  Parameters and state-dict names are nn.Linear's."""
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        cast = self.__dict__.get("_cast")
+        if cast is not None:
+            return F.linear(x, cast[0], cast[1])
+        return super().forward(x)
 
 
 class RMSNorm(nn.Module):
@@ -141,8 +153,10 @@ class BottleneckPatchEmbedNHWC(nn.Module):
         p = self.patch_size[0]
         gh, gw = self.grid_size
         patches = x.reshape(b, cin, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5).reshape(b, gh, gw, cin * p * p)
-        h = F.linear(patches, self.proj1.weight.view(self.proj1.out_channels, -1))
-        return F.linear(h, self.proj2.weight.view(self.proj2.out_channels, -1), self.proj2.bias)
+        cast = self.__dict__.get("_cast")
+        w1, w2, b2 = cast if cast is not None else (self.proj1.weight, self.proj2.weight, self.proj2.bias)
+        h = F.linear(patches, w1.view(self.proj1.out_channels, -1))
+        return F.linear(h, w2.view(self.proj2.out_channels, -1), b2)
 
 
 class TimestepEmbedder(nn.Module):
@@ -152,9 +166,9 @@ class TimestepEmbedder(nn.Module):
         super().__init__()
         self.frequency_embedding_size = frequency_embedding_size
         self.mlp = nn.Sequential(
-            nn.Linear(frequency_embedding_size, hidden_size, bias=True),
+            CastLinear(frequency_embedding_size, hidden_size, bias=True),
             nn.SiLU(),
-            nn.Linear(hidden_size, hidden_size, bias=True),
+            CastLinear(hidden_size, hidden_size, bias=True),
         )
 
     @staticmethod
@@ -202,11 +216,11 @@ class WorkspaceAttention(nn.Module):
             raise ValueError(f"dim={dim} must be divisible by num_heads={num_heads}")
         self.num_heads = num_heads
         self.head_dim = dim // num_heads
-        self.qkv = nn.Linear(dim, dim * 3, bias=qkv_bias)
+        self.qkv = CastLinear(dim, dim * 3, bias=qkv_bias)
         self.q_norm = RMSNorm(self.head_dim) if qk_norm else nn.Identity()
         self.k_norm = RMSNorm(self.head_dim) if qk_norm else nn.Identity()
         self.attn_drop = nn.Dropout(attn_drop)
-        self.proj = nn.Linear(dim, dim)
+        self.proj = CastLinear(dim, dim)
         self.proj_drop = nn.Dropout(proj_drop)
         self.attn_backend = attn_backend
         # q/k norm + RoPE + attention as one HIP pass (jit_thc::qk_norm_rope_attention) where it applies
@@ -274,8 +288,8 @@ class SwiGLUFFN(nn.Module):
     def __init__(self, dim: int, hidden_dim: int, drop: float = 0.0, bias: bool = True) -> None:
         super().__init__()
         hidden = int(hidden_dim * 2 / 3)
-        self.w12 = nn.Linear(dim, 2 * hidden, bias=bias)
-        self.w3 = nn.Linear(hidden, dim, bias=bias)
+        self.w12 = CastLinear(dim, 2 * hidden, bias=bias)
+        self.w3 = CastLinear(hidden, dim, bias=bias)
         self.ffn_dropout = nn.Dropout(drop)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -327,7 +341,7 @@ class FinalLayerSharedAdaLN(nn.Module):
     def __init__(self, hidden_size: int, patch_size: int, out_channels: int) -> None:
         super().__init__()
         self.norm_final = RMSNorm(hidden_size)
-        self.linear = nn.Linear(hidden_size, patch_size * patch_size * out_channels, bias=True)
+        self.linear = CastLinear(hidden_size, patch_size * patch_size * out_channels, bias=True)
 
     def forward(self, x: torch.Tensor, t2: torch.Tensor) -> torch.Tensor:
         shift, scale = t2.chunk(2, dim=1)
@@ -462,13 +476,15 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
             for i in range(depth)
         )
         self.final_layer = FinalLayerSharedAdaLN(hidden_size, patch_size, self.out_channels)
-        self.shared_adaLN_modulation = nn.Sequential(nn.SiLU(), nn.Linear(hidden_size, 6 * hidden_size, bias=True))
-        self.shared_final_modulation = nn.Sequential(nn.SiLU(), nn.Linear(hidden_size, 2 * hidden_size, bias=True))
+        self.shared_adaLN_modulation = nn.Sequential(nn.SiLU(), CastLinear(hidden_size, 6 * hidden_size, bias=True))
+        self.shared_final_modulation = nn.Sequential(nn.SiLU(), CastLinear(hidden_size, 2 * hidden_size, bias=True))
         self.initialize_weights()
         self.shared_read = SharedLocalRead(high_grid, workspace_grid, hidden_size, self.pool_groups, use_softmax_write=True)
         self.use_lazy = bool(use_lazy)
         # decoder head as one HIP pass (jit_thc::decoder_head) where it applies
         self.fused_decoder = True
+        # inference under autocast with fp32 parameters: all weight conversions in one launch
+        self.batched_weight_cast = True
 
     # -- initialisation (local_thc.py:944-970, :1004-1007) ------------------------------------------
     def initialize_weights(self) -> None:
@@ -532,10 +548,8 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
         ):
             # RMSNorm + modulate + linear + unpatchify in one pass (jit_thc::decoder_head): y never reaches memory
             shift, scale = t2.chunk(2, dim=1)
-            return ops.decoder_head(
-                x, fl.norm_final.weight, shift, scale, fl.linear.weight, fl.linear.bias, fl.norm_final.eps, hh,
-                self.patch_size,
-            )
+            lw, lb = fl.linear.__dict__.get("_cast") or (fl.linear.weight, fl.linear.bias)
+            return ops.decoder_head(x, fl.norm_final.weight, shift, scale, lw, lb, fl.norm_final.eps, hh, self.patch_size)
         return self.unpatchify(fl(x, t2))
 
     def forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
@@ -560,7 +574,56 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
 
     def forward(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor, use_lazy: bool | None = None) -> torch.Tensor:
         lazy = self.use_lazy if use_lazy is None else use_lazy
-        return self.forward_lazy(x, t, y) if lazy else self.forward_naive(x, t, y)
+        with self._converted_weights():
+            return self.forward_lazy(x, t, y) if lazy else self.forward_naive(x, t, y)
+
+    def _conversion_targets(self) -> list[tuple[nn.Module, list[torch.Tensor]]]:
+        """Modules whose weights autocast would convert on every forward, with the tensors it would convert."""
+        out: list[tuple[nn.Module, list[torch.Tensor]]] = [
+            (m, [m.weight, m.bias] if m.bias is not None else [m.weight])
+            for m in self.modules()
+            if isinstance(m, CastLinear)
+        ]
+        pe = self.x_embedder
+        if pe.proj2.bias is not None:
+            out.append((pe, [pe.proj1.weight, pe.proj2.weight, pe.proj2.bias]))
+        return out
+
+    @contextmanager
+    def _converted_weights(self):
+        """Under a bf16 / fp16 CUDA autocast without autograd and with fp32 parameters (inference), convert every
+        linear weight once, in one launch (ops.BatchedCast), for this forward: the values autocast's ~150
+        per-layer conversions would produce.  Otherwise (training, no autocast, 16-bit parameters) a no-op."""
+        targets = self._conversion_targets() if self.batched_weight_cast else []
+        dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
+        tensors = [t for _, ts in targets for t in ts]
+        usable = (
+            bool(tensors)
+            and dt in (torch.bfloat16, torch.float16)
+            and not torch.is_grad_enabled()
+            and all(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() for t in tensors)
+        )
+        bc = self.__dict__.get("_batched_cast") if usable else None
+        key = (dt, tuple((t.data_ptr(), t.numel()) for t in tensors)) if usable else None
+        if usable and (bc is None or bc.key != key):
+            if torch.cuda.is_current_stream_capturing():  # the table is built eagerly, outside a capture
+                usable = False
+            else:
+                bc = ops.BatchedCast(tensors, dt)
+                self.__dict__["_batched_cast"] = bc
+        if not usable:
+            yield
+            return
+        outs = bc()
+        i = 0
+        for m, ts in targets:
+            m.__dict__["_cast"] = tuple(outs[i : i + len(ts)])
+            i += len(ts)
+        try:
+            yield
+        finally:
+            for m, _ in targets:
+                m.__dict__.pop("_cast", None)
 
 
 class SharedReadFusedFinal12LocalTHCSharedAdaLNJiT(SharedReadLocalTHCSharedAdaLNJiT):

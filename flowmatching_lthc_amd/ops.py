@@ -1107,6 +1107,53 @@ def _backward_decoder(ctx, grad):
 torch.library.register_autograd(decoder_head, _backward_decoder, setup_context=_setup_decoder_ctx)
 
 
+# ---------------------------------------------------------------------------
+# BATCHED WEIGHT CONVERSION (autocast's per-forward weight casts in one launch)
+# ---------------------------------------------------------------------------
+_CAST_BLOCK = 2048  # elements per block of lthc_cast_many
+
+
+class BatchedCast:
+    """Converts a fixed list of contiguous fp32 tensors to `dtype` (round to nearest even, autocast's values) in
+    one launch.  The outputs are views of one flat buffer, rewritten on every call; the conversion table is built
+    once and holds the sources' addresses, so the sources are kept alive here and `key` identifies them."""
+
+    def __init__(self, tensors: Sequence[Tensor], dtype: torch.dtype):
+        if dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError(f"dtype must be bf16 or fp16, got {dtype}")
+        if not tensors:
+            raise ValueError("no tensors to convert")
+        dev = tensors[0].device
+        for t in tensors:
+            if t.dtype != torch.float32 or not t.is_contiguous() or t.device != dev:
+                raise ValueError("sources must be contiguous fp32 tensors on one device")
+        self.key = (dtype, tuple((t.data_ptr(), t.numel()) for t in tensors))
+        self.dtype = dtype
+        self._src = list(tensors)
+        entries, block_map, off, nblk = [], [], 0, 0
+        for i, t in enumerate(tensors):
+            n = t.numel()
+            nb = (n + _CAST_BLOCK - 1) // _CAST_BLOCK
+            entries.append((t.data_ptr(), n, off, nblk))
+            block_map.extend([i] * nb)
+            off += (n + 7) // 8 * 8
+            nblk += nb
+        self.nblocks = nblk
+        self.buf = torch.empty((max(off, 8),), device=dev, dtype=dtype)
+        self.entries = torch.tensor(entries, dtype=torch.int64).to(dev)
+        self.block_map = torch.tensor(block_map, dtype=torch.int32).to(dev)
+        self.outs = [self.buf[e[2]:e[2] + t.numel()].view(t.shape) for e, t in zip(entries, tensors)]
+
+    def __call__(self) -> list[Tensor]:
+        with _on_device(self.buf):
+            rc = _abi.load().lthc_cast_many(
+                self.entries.data_ptr(), self.block_map.data_ptr(), self.nblocks, self.buf.data_ptr(),
+                _abi.code(self.buf), _abi.stream_of(self.buf),
+            )  # fmt: skip
+        _abi.check(rc, "lthc_cast_many")
+        return self.outs
+
+
 # Reference-style aliases (local_thc_triton_kernels.py exports these names).
 triton_final_accumulate_b4_traceable = final_accumulate_b4_traceable
 triton_final_accumulate_b4_12_traceable = final_accumulate_b4_12_traceable

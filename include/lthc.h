@@ -269,6 +269,19 @@ int lthc_decoder_fwd(const void* x, int x_dtype, const void* norm_weight, int nw
                      float eps, void* stream);
 
 /*
+ * BATCHED WEIGHT CONVERSION (no reference op: autocast converts each fp32
+ * weight in its own kernel on every forward).  entries: device array of
+ * {const float* src; int64_t numel; int64_t dst_offset; int64_t first_block}
+ * (32 bytes each, 8-byte aligned); block_map: device int32 [nblocks], the
+ * entry of each block.  Block b converts elements
+ * [(b - first_block) * 2048, +2048) of its entry to dst_dtype (bf16 or fp16,
+ * round to nearest even) at dst + dst_offset.  dst 16-byte aligned, every
+ * dst_offset a multiple of 8 elements.
+ */
+int lthc_cast_many(const void* entries, const void* block_map, int64_t nblocks, void* dst, int dst_dtype,
+                   void* stream);
+
+/*
  * SWIGLU GATE (no reference op: SwiGLUFFN.forward's chunk + silu + mul,
  * local_thc.py:267-269, three eager passes):
  *   out[r, f] = r(r(a / (1 + exp(-a))) * v),  a = x[r, f], v = x[r, F + f]
