@@ -32,6 +32,7 @@ EXPORTS = (
     "lthc_weight_grad_workspace_bytes",
     "lthc_weight_grad",
     "lthc_gamma",
+    "lthc_gamma_rounded",
     "lthc_recur_fwd",
     "lthc_recur_bwd_workspace_bytes",
     "lthc_recur_bwd",
@@ -80,6 +81,7 @@ def load() -> ctypes.CDLL:
         "lthc_materialise_fwd": [vp, pp, ci, pp, ci, vp, i64, i64, i64, i64, ci, vp],
         "lthc_weight_grad": [vp, pp, ci, vp, i64, i64, i64, i64, ci, vp, sz, vp],
         "lthc_gamma": [vp, pp, ci, vp, ci, i64, i64, ci, vp],
+        "lthc_gamma_rounded": [vp, ci, pp, ci, vp, ci, i64, i64, ci, vp],
         "lthc_recur_fwd": [vp, vp, ci, vp, ci, vp, i64, i64, vp],
         "lthc_recur_bwd": [vp, vp, vp, ci, vp, ci, vp, vp, i64, i64, vp, sz, vp],
         "lthc_ws_accumulate_fwd": [vp, pp, ci, vp, ci, vp, i64, i64, ci, vp],

@@ -215,6 +215,14 @@ LTHC_DEV float load_w(const void* __restrict__ p, int dt, int64_t i) {
   return widen1<LTHC_F16>(h);
 }
 
+// Round one value to format DT (round to nearest even; identity for fp32).
+template <int DT>
+LTHC_DEV float round_w(float v) {
+  if constexpr (DT == LTHC_F32) return v;
+  else if constexpr (DT == LTHC_BF16) return static_cast<float>(static_cast<__bf16>(v));
+  else return static_cast<float>(static_cast<_Float16>(v));
+}
+
 LTHC_DEV void store_w(void* __restrict__ p, int dt, int64_t i, float v) {
   if (dt == LTHC_F32) {
     static_cast<float*>(p)[i] = v;
@@ -831,6 +839,29 @@ __global__ __launch_bounds__(256) void gamma_kernel(const void* __restrict__ alp
   for (int k = 0; k < K; ++k)
     s = fmaf(load_w(alpha, wdt, static_cast<int64_t>(c) * K + k), load_w(beta.p[l], wdt, static_cast<int64_t>(c) * K + k), s);
   store_w(gamma, odt, i, s);
+}
+
+// ---------------------------------------------------------------------------
+// GAMMA with the eager dtype sequence (LayerLocalWrite.gamma_from_alpha under
+// autocast, local_thc.py:1278-1283 with alpha cast at :1326):
+//   gamma[l, c] = r(sum_k r(r(alpha[c,k]) * r(beta_l[c,k])))   sum in fp32, k = 0..K-1
+// r = round to the output dtype (identity for fp32).
+// ---------------------------------------------------------------------------
+template <int ODT>
+__global__ __launch_bounds__(256) void gamma_rounded_kernel(const void* __restrict__ alpha, int adt, PtrPack beta,
+                                                            int bdt, void* __restrict__ gamma, int C, int K, int L) {
+#pragma clang fp contract(off)  // the product is rounded before it is summed
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(L) * C) return;
+  const int l = static_cast<int>(i / C);
+  const int c = static_cast<int>(i - static_cast<int64_t>(l) * C);
+  float s = 0.f;
+  for (int k = 0; k < K; ++k) {
+    const float a = round_w<ODT>(load_w(alpha, adt, static_cast<int64_t>(c) * K + k));
+    const float b = round_w<ODT>(load_w(beta.p[l], bdt, static_cast<int64_t>(c) * K + k));
+    s += round_w<ODT>(a * b);
+  }
+  store_w(gamma, ODT, i, s);
 }
 
 // ---------------------------------------------------------------------------
@@ -1555,6 +1586,29 @@ int lthc_gamma(const void* alpha, const void* const* beta, int w_dtype, void* ga
   const int64_t n = static_cast<int64_t>(L) * C;
   gamma_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
       alpha, bp, w_dtype, gamma, out_dtype, static_cast<int>(C), static_cast<int>(K), L);
+  return check_launch(fn);
+}
+
+int lthc_gamma_rounded(const void* alpha, int a_dtype, const void* const* beta, int b_dtype, void* gamma,
+                       int out_dtype, int64_t C, int64_t K, int L, void* stream) {
+  static const char* fn = "lthc_gamma_rounded";
+  g_last_error.clear();
+  if (int rc = check_layers(fn, L)) return rc;
+  if (C <= 0 || K <= 0 || K > 1024 || C > (1 << 24)) return fail(LTHC_ERR_INVALID, fn, "C or K out of range");
+  if (!valid_dtype(a_dtype) || !valid_dtype(b_dtype) || !valid_dtype(out_dtype))
+    return fail(LTHC_ERR_INVALID, fn, "unknown dtype code");
+  if (alpha == nullptr || gamma == nullptr || beta == nullptr) return fail(LTHC_ERR_INVALID, fn, "a NULL pointer");
+  PtrPack bp;
+  for (int l = 0; l < L; ++l) {
+    if (beta[l] == nullptr) return fail(LTHC_ERR_INVALID, fn, "beta[" + std::to_string(l) + "] is NULL");
+    bp.p[l] = beta[l];
+  }
+  const int64_t n = static_cast<int64_t>(L) * C;
+  dispatch_dtype(out_dtype, [&](auto d) {
+    gamma_rounded_kernel<decltype(d)::value><<<static_cast<unsigned>((n + 255) / 256), 256, 0,
+                                               static_cast<hipStream_t>(stream)>>>(
+        alpha, a_dtype, bp, b_dtype, gamma, static_cast<int>(C), static_cast<int>(K), L);
+  });
   return check_launch(fn);
 }
 

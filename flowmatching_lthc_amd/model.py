@@ -386,11 +386,13 @@ class SharedReadLocalTHCSharedAdaLNJiTBlock(nn.Module):
         return ops.lazy_workspace_update(z, dz, gamma)
 
     def lazy_workspace_step(
-        self, z: torch.Tensor, dz: torch.Tensor, shared_read: SharedLocalRead
+        self, z: torch.Tensor, dz: torch.Tensor, shared_read: SharedLocalRead, gamma: torch.Tensor | None = None
     ) -> tuple[torch.Tensor, torch.Tensor]:
         """(lazy_workspace_update(z, dz), dz) for the lazy forward, where dz is also materialised at the end;
-        the backward writes dz's whole gradient in one recurrence-backward pass (ops.lazy_workspace_step)."""
-        gamma = self.write.gamma_from_alpha(shared_read.alpha(dtype=dz.dtype))
+        the backward writes dz's whole gradient in one recurrence-backward pass (ops.lazy_workspace_step).
+        gamma: this layer's gamma_from_alpha(shared_read.alpha(dz.dtype)) when the caller has computed it."""
+        if gamma is None:
+            gamma = self.write.gamma_from_alpha(shared_read.alpha(dtype=dz.dtype))
         return ops.lazy_workspace_step(z, dz, gamma)
 
 
@@ -558,12 +560,30 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
         # and the recurrence steps are the fused-backward forms: same values, x0's and each dZ_l's gradient
         # from one kernel instead of a kernel plus autograd's add.
         x0, z = self.shared_read.read_with_residual(self.x_embedder(x))
-        dz_list = []
-        for block in self.blocks:
+        dz_list, gammas = [], None
+        for i, block in enumerate(self.blocks):
             dz = block.branch_update(z, t6, self.workspace_rope)
-            z, dz = block.lazy_workspace_step(z, dz, self.shared_read)
+            if i == 0:
+                gammas = self._all_gammas(dz)
+            if gammas is None:  # the reference's hook signature
+                z, dz = block.lazy_workspace_step(z, dz, self.shared_read)
+            else:
+                z, dz = block.lazy_workspace_step(z, dz, self.shared_read, gammas[i])
             dz_list.append(dz)
         return self._decode(self.final_accumulate_reference(x0, dz_list), t2)
+
+    def _all_gammas(self, dz: torch.Tensor) -> list[torch.Tensor] | None:
+        """Every block's gamma_from_alpha(shared_read.alpha(dz.dtype)) in one launch (ops.lazy_gamma_rounded: the
+        same dtype sequence), or None where it does not apply (CPU, grouped write weights, another block type)."""
+        writes = [blk.write for blk in self.blocks]
+        own_hooks = all(  # no block replaces the hook (subclass or instance override): it takes the gamma argument
+            type(blk).lazy_workspace_step is SharedReadLocalTHCSharedAdaLNJiTBlock.lazy_workspace_step
+            and "lazy_workspace_step" not in blk.__dict__
+            for blk in self.blocks
+        )
+        if not dz.is_cuda or not own_hooks or self.shared_read.group_dim != 1 or any(w.group_dim != 1 for w in writes):
+            return None
+        return list(ops.lazy_gamma_rounded(self.shared_read.alpha(), [w.write_weight for w in writes], dz.dtype).unbind(0))
 
     def forward_naive(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         t6, t2 = self._conditioning(t, y)

@@ -885,6 +885,67 @@ torch.library.register_autograd(lazy_gamma_stack, _backward_gamma, setup_context
 
 
 # ---------------------------------------------------------------------------
+# GAMMA OF EVERY LAYER WITH THE EAGER DTYPE SEQUENCE (one launch for the block hooks' gamma_from_alpha)
+# ---------------------------------------------------------------------------
+def lazy_gamma_rounded_eager(alpha: Tensor, betas: Sequence[Tensor], dtype: torch.dtype) -> Tensor:
+    """[L, C] of (alpha.to(dtype) * beta_l.to(dtype)).sum(-1): gamma_from_alpha (local_thc.py:1278-1283) for each
+    layer, alpha being the shared read's softmax cast to the workspace dtype (:1326)."""
+    a = alpha.to(dtype)
+    return torch.stack([(a * b.to(dtype)).sum(dim=-1) for b in betas])
+
+
+@torch.library.custom_op("jit_thc::lazy_gamma_rounded", mutates_args=())
+def lazy_gamma_rounded(alpha: Tensor, betas: list[Tensor], dtype: torch.dtype) -> Tensor:
+    """[L, C] in `dtype` of r(sum_k r(r(alpha) r(beta_l))), r = round to `dtype`, the sum in fp32: the block hooks'
+    gamma_from_alpha(shared_read.alpha(dtype)) for all layers in one launch."""
+    _on_gpu(alpha, *betas)
+    if alpha.dim() != 2 or not betas or any(tuple(b.shape) != tuple(alpha.shape) for b in betas):
+        raise ValueError(f"alpha [C,K] and L betas of the same shape expected, got {tuple(alpha.shape)}")
+    if not 1 <= len(betas) <= _abi.MAX_LAYERS:
+        raise ValueError(f"depth {len(betas)} outside 1..{_abi.MAX_LAYERS}")
+    bd = betas[0].dtype
+    betas = [b.contiguous() if b.dtype == bd else b.to(bd).contiguous() for b in betas]
+    alpha = alpha.contiguous()
+    c, k = alpha.shape
+    out = torch.empty((len(betas), c), device=alpha.device, dtype=dtype)
+    with _on_device(alpha):
+        rc = _abi.load().lthc_gamma_rounded(
+            alpha.data_ptr(), _abi.code(alpha), _abi.ptr_array(betas), _abi.code(betas[0]), out.data_ptr(),
+            _abi.code(out), c, k, len(betas), _abi.stream_of(alpha),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_gamma_rounded")
+    return out
+
+
+@lazy_gamma_rounded.register_fake
+def _(alpha: Tensor, betas: list[Tensor], dtype: torch.dtype) -> Tensor:
+    return alpha.new_empty((len(betas), alpha.shape[0]), dtype=dtype)
+
+
+def _setup_gamma_rounded_ctx(ctx, inputs, output):
+    alpha, betas, dtype = inputs
+    ctx.save_for_backward(alpha, *betas)
+    ctx.dtype = dtype
+
+
+def _backward_gamma_rounded(ctx, grad):
+    alpha, *betas = ctx.saved_tensors
+    need_a, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    with torch.enable_grad():
+        a = alpha.detach().requires_grad_(bool(need_a))
+        bs = [b.detach().requires_grad_(bool(need_b)) for b in betas]
+        out = lazy_gamma_rounded_eager(a, bs, ctx.dtype)
+        wanted = ([a] if need_a else []) + (bs if need_b else [])
+        got = list(torch.autograd.grad([out], wanted, [grad], allow_unused=True)) if wanted else []
+    ga = got.pop(0) if need_a else None
+    gb = got if need_b else None
+    return ga, gb, None
+
+
+torch.library.register_autograd(lazy_gamma_rounded, _backward_gamma_rounded, setup_context=_setup_gamma_rounded_ctx)
+
+
+# ---------------------------------------------------------------------------
 # FINAL-LAYER RMSNORM + MODULATE (no reference op: FinalLayerSharedAdaLN's
 # norm_final + modulate, local_thc.py:870-873, is eager torch)
 # ---------------------------------------------------------------------------

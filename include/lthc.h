@@ -138,6 +138,18 @@ int lthc_gamma(const void* alpha, const void* const* beta, int w_dtype, void* ga
                int64_t C, int64_t K, int L, void* stream);
 
 /*
+ * GAMMA WITH THE EAGER DTYPE SEQUENCE, all layers in one launch: for the
+ * block hook LayerLocalWrite.gamma_from_alpha(shared_read.alpha(dz.dtype))
+ * (local_thc.py:1278-1283, :1325-1327) evaluated in out_dtype,
+ *   gamma[l, c] = r(sum_k r(r(alpha[c,k]) * r(beta_l[c,k])))
+ * with r = round to out_dtype (identity for fp32) and the sum in fp32 over
+ * k = 0..K-1.  alpha [C, K] in a_dtype (e.g. the fp32 softmax of the read
+ * logits), beta_l [C, K] in b_dtype, gamma [L, C] in out_dtype.
+ */
+int lthc_gamma_rounded(const void* alpha, int a_dtype, const void* const* beta, int b_dtype, void* gamma,
+                       int out_dtype, int64_t C, int64_t K, int L, void* stream);
+
+/*
  * LAZY WORKSPACE RECURRENCE STEP   z_next[r,c] = z[r,c] + gamma[c] * dz[r,c]
  * Replaces SharedReadLocalTHCSharedAdaLNJiTBlock.lazy_workspace_update
  * (local_thc.py:1325-1328); rows = B*M.  Computed as fma(gamma, dz, z).
