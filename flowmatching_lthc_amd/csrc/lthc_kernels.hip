@@ -841,6 +841,24 @@ __global__ __launch_bounds__(256) void gamma_kernel(const void* __restrict__ alp
   store_w(gamma, odt, i, s);
 }
 
+// The same for K == 16 and 16-byte aligned rows: each row is one vector load
+// (four for fp32), all issued before the 16 FMAs (the k order is unchanged).
+template <int WDT, int ODT>
+__global__ __launch_bounds__(256) void gamma16_kernel(const void* __restrict__ alpha, PtrPack beta,
+                                                      void* __restrict__ gamma, int C, int L) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(L) * C) return;
+  const int l = static_cast<int>(i / C);
+  const int c = static_cast<int>(i - static_cast<int64_t>(l) * C);
+  float a[kK], b[kK];
+  load_wvec<WDT, kK>(alpha, static_cast<int64_t>(c) * kK, a);
+  load_wvec<WDT, kK>(beta.p[l], static_cast<int64_t>(c) * kK, b);
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < kK; ++k) s = fmaf(a[k], b[k], s);
+  store_w(gamma, ODT, i, s);
+}
+
 // ---------------------------------------------------------------------------
 // GAMMA with the eager dtype sequence (LayerLocalWrite.gamma_from_alpha under
 // autocast, local_thc.py:1278-1283 with alpha cast at :1326):
@@ -1584,8 +1602,20 @@ int lthc_gamma(const void* alpha, const void* const* beta, int w_dtype, void* ga
     bp.p[l] = beta[l];
   }
   const int64_t n = static_cast<int64_t>(L) * C;
-  gamma_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, static_cast<hipStream_t>(stream)>>>(
-      alpha, bp, w_dtype, gamma, out_dtype, static_cast<int>(C), static_cast<int>(K), L);
+  const unsigned blocks = static_cast<unsigned>((n + 255) / 256);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  bool rows16 = K == kK && aligned(alpha, 16);
+  for (int l = 0; l < L; ++l) rows16 = rows16 && aligned(beta[l], 16);
+  if (rows16) {
+    dispatch_dtype(w_dtype, [&](auto wd) {
+      dispatch_dtype(out_dtype, [&](auto od) {
+        gamma16_kernel<decltype(wd)::value, decltype(od)::value><<<blocks, 256, 0, st>>>(alpha, bp, gamma,
+                                                                                         static_cast<int>(C), L);
+      });
+    });
+    return check_launch(fn);
+  }
+  gamma_kernel<<<blocks, 256, 0, st>>>(alpha, bp, w_dtype, gamma, out_dtype, static_cast<int>(C), static_cast<int>(K), L);
   return check_launch(fn);
 }
 
