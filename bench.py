@@ -513,6 +513,10 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
     T = B * H * H * C
     W = B * G * G * C
     fused_bwd = 2 * (3 * T + 3 * L * W)
+    # per-op compulsory bytes: materialise backward e(T + 2LW) (gdZ and gbeta from one read of G_L), recurrence
+    # backward e(6LW) (per layer g, dz, the branch gradient and the materialisation's gradient in, two out), read
+    # backward e(3T + W) (G_L, gZ0 and X0 in, dX0 out)
+    per_op_bwd = 2 * (4 * T + 8 * L * W + W)
     fwd_ms, step_ms = (graph_fwd, graph_step) if graph_error is None else (eager_fwd, eager_step)
     bwd_ms = step_ms - fwd_ms
     return {
@@ -529,8 +533,12 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
         "eager_fwd_bwd_ms": round(eager_step, 4),
         "bwd_single_pass_bytes": fused_bwd,
         "bwd_single_pass_GBps": round(fused_bwd / (bwd_ms * 1e-3) / 1e9, 1),
-        "byte_definition": "bwd_single_pass_bytes = e*(3T + 3LW): the compulsory bytes of a fused backward "
-        "(read G_L, X0, H stack, dZ stack; write dX0, dZ-grad stack); the ops launched move more",
+        "bwd_per_op_bytes": per_op_bwd,
+        "bwd_per_op_GBps": round(per_op_bwd / (bwd_ms * 1e-3) / 1e9, 1),
+        "byte_definition": "bwd_single_pass_bytes = e*(3T + 3LW): the compulsory bytes of a fused single-pass backward "
+        "(read G_L, X0, H stack, dZ stack; write dX0, dZ-grad stack); bwd_per_op_bytes = e*(4T + 8LW + W): each "
+        "backward op's compulsory bytes (materialise e(T+2LW), L recurrence steps e(6LW), read e(3T+W)); the "
+        "launched ops move more (G_L is read twice by the materialise backward)",
     }
 
 
