@@ -449,8 +449,8 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
         gam = ops.lazy_gamma_stack(alpha.to(bf16), torch.stack([b.to(bf16) for b in betas])).unbind(0)
         zs, dzv = [z], []
         for l in range(L):
-            z, d = ops.lazy_workspace_step(z, dzs[l], gam[l])  # as the model's forward_lazy
-            zs.append(z)
+            z, zb, d = ops.lazy_workspace_step(z, dzs[l], gam[l], split=True)  # as the model's forward_lazy
+            zs.append(zb)  # the next branch's input
             dzv.append(d)
         if L == 12:
             xl = ops.final_accumulate_b4_12_traceable(x0v, *dzv, *betas)

@@ -33,9 +33,11 @@ EXPORTS = (
     "lthc_weight_grad",
     "lthc_gamma",
     "lthc_gamma_rounded",
+    "lthc_gamma_rounded_bwd",
     "lthc_recur_fwd",
     "lthc_recur_bwd_workspace_bytes",
     "lthc_recur_bwd",
+    "lthc_recur_bwd_sum",
     "lthc_ws_accumulate_fwd",
     "lthc_ws_accumulate_bwd_workspace_bytes",
     "lthc_ws_accumulate_bwd",
@@ -82,8 +84,10 @@ def load() -> ctypes.CDLL:
         "lthc_weight_grad": [vp, pp, ci, vp, i64, i64, i64, i64, ci, vp, sz, vp],
         "lthc_gamma": [vp, pp, ci, vp, ci, i64, i64, ci, vp],
         "lthc_gamma_rounded": [vp, ci, pp, ci, vp, ci, i64, i64, ci, vp],
+        "lthc_gamma_rounded_bwd": [vp, vp, ci, pp, ci, vp, pp, ci, i64, i64, ci, vp],
         "lthc_recur_fwd": [vp, vp, ci, vp, ci, vp, i64, i64, vp],
         "lthc_recur_bwd": [vp, vp, vp, ci, vp, ci, vp, vp, i64, i64, vp, sz, vp],
+        "lthc_recur_bwd_sum": [vp, vp, vp, vp, ci, vp, ci, vp, vp, vp, i64, i64, vp, sz, vp],
         "lthc_ws_accumulate_fwd": [vp, pp, ci, vp, ci, vp, i64, i64, ci, vp],
         "lthc_ws_accumulate_bwd": [vp, pp, ci, vp, ci, pp, vp, i64, i64, ci, vp, sz, vp],
         "lthc_norm_modulate_fwd": [vp, ci, vp, ci, vp, vp, i64, vp, vp, i64, i64, i64, ctypes.c_float, vp],

@@ -882,6 +882,33 @@ __global__ __launch_bounds__(256) void gamma_rounded_kernel(const void* __restri
   store_w(gamma, ODT, i, s);
 }
 
+// Its backward, the eager autograd of that sequence: with a = r(alpha),
+// b_l = r(beta_l) and g_l = grad[l, c],
+//   gbeta_l[c,k] = r(g_l * a[c,k])
+//   galpha[c,k]  = r(... r(r(g_{L-1} b_{L-1}) + r(g_{L-2} b_{L-2})) ... + r(g_0 b_0))
+// the L products being summed into a's gradient in the order autograd
+// delivers them (last layer first), each partial sum rounded.
+template <int ODT>
+__global__ __launch_bounds__(256) void gamma_rounded_bwd_kernel(const void* __restrict__ grad,
+                                                                const void* __restrict__ alpha, int adt,
+                                                                PtrPack beta, int bdt, void* __restrict__ galpha,
+                                                                PtrPack gbeta, int C, int K, int L) {
+#pragma clang fp contract(off)
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(C) * K) return;
+  const int c = static_cast<int>(i / K);
+  const float a = round_w<ODT>(load_w(alpha, adt, i));
+  float acc = 0.f;
+  for (int l = L - 1; l >= 0; --l) {
+    const float g = load_w(grad, ODT, static_cast<int64_t>(l) * C + c);
+    const float b = round_w<ODT>(load_w(beta.p[l], bdt, i));
+    const float pa = round_w<ODT>(g * b);
+    acc = l == L - 1 ? pa : round_w<ODT>(acc + pa);
+    if (gbeta.p[l] != nullptr) store_w(const_cast<void*>(gbeta.p[l]), bdt, i, round_w<ODT>(g * a));
+  }
+  if (galpha != nullptr) store_w(galpha, adt, i, acc);
+}
+
 // ---------------------------------------------------------------------------
 // RECURRENCE: z_next = fma(gamma, dz, z).  Block = 64 channel quads x 4 row
 // lanes; each thread keeps its 4 gammas.  A block handles chunks of 4 * RU
@@ -960,13 +987,15 @@ __global__ __launch_bounds__(256) void recur_fwd_flat_kernel(const void* __restr
 
 // RECURRENCE BACKWARD: gdz = gamma * g (+ gadd, HAS_ADD); partial[4*by + lane_row, c]
 // = sum g*dz over the rows the thread visits.  Grid and row order as
-// recur_fwd_kernel.
-template <int DT, typename Off, bool HAS_ADD>
+// recur_fwd_kernel.  HAS_G2: g is the sum of two gradients, g + g2 rounded to
+// DT (the value of autograd's add of the two), which is also written to gsum.
+template <int DT, typename Off, bool HAS_ADD, bool HAS_G2 = false>
 __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__ g, const void* __restrict__ dz,
                                                         const void* __restrict__ gadd,
                                                         const void* __restrict__ gamma, int gdt,
                                                         void* __restrict__ gdz, float* __restrict__ partial,
-                                                        int64_t rows, int C) {
+                                                        int64_t rows, int C, const void* __restrict__ g2 = nullptr,
+                                                        void* __restrict__ gsum = nullptr) {
   constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int c0 = (blockIdx.x * 64 + (t & 63)) * 4;
@@ -978,13 +1007,14 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
   const int64_t re = rows;
   const int64_t S = static_cast<int64_t>(4 * kRU) * gridDim.y;
   for (int64_t r0 = static_cast<int64_t>(blockIdx.y) * 4 * kRU + (t >> 6); r0 < re; r0 += S) {
-    Raw<DT, 4> ar[kRU], dr[kRU], xr[HAS_ADD ? kRU : 1];
+    Raw<DT, 4> ar[kRU], dr[kRU], xr[HAS_ADD ? kRU : 1], br[HAS_G2 ? kRU : 1];
     Off off[kRU];
 #pragma unroll
     for (int u = 0; u < kRU; ++u) {
       const int64_t r = std::min(r0 + 4 * u, re - 1);
       off[u] = static_cast<Off>((r * C + c0) * ES);
       load_at<DT, 4, true>(g, off[u], ar[u]);
+      if constexpr (HAS_G2) load_at<DT, 4, true>(g2, off[u], br[u]);
       load_at<DT, 4, true>(dz, off[u], dr[u]);
       if constexpr (HAS_ADD) load_at<DT, 4, true>(gadd, off[u], xr[u]);
     }
@@ -994,6 +1024,22 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
       if (r0 + 4 * u < re) {
         float a[4], d[4], o4[4];
         unpack_raw<DT, 4>(ar[u], a);
+        if constexpr (HAS_G2) {
+          float b[4];
+          unpack_raw<DT, 4>(br[u], b);
+#pragma unroll
+          for (int v = 0; v < 4; ++v) a[v] += b[v];
+          Raw<DT, 4> sr;  // the sum rounded to DT, stored and used from here on
+          if constexpr (DT == LTHC_F32) {
+#pragma unroll
+            for (int v = 0; v < 4; ++v) sr.w[v] = __float_as_uint(a[v]);
+          } else {
+            sr.w[0] = pack2<DT>(a[0], a[1]);
+            sr.w[1] = pack2<DT>(a[2], a[3]);
+          }
+          unpack_raw<DT, 4>(sr, a);
+          store_at<DT, 4, true>(gsum, off[u], a);
+        }
         unpack_raw<DT, 4>(dr[u], d);
         if constexpr (HAS_ADD) {
           unpack_raw<DT, 4>(xr[u], o4);
@@ -1642,6 +1688,31 @@ int lthc_gamma_rounded(const void* alpha, int a_dtype, const void* const* beta, 
   return check_launch(fn);
 }
 
+int lthc_gamma_rounded_bwd(const void* grad, const void* alpha, int a_dtype, const void* const* beta, int b_dtype,
+                           void* galpha, void* const* gbeta, int out_dtype, int64_t C, int64_t K, int L,
+                           void* stream) {
+  static const char* fn = "lthc_gamma_rounded_bwd";
+  g_last_error.clear();
+  if (int rc = check_layers(fn, L)) return rc;
+  if (C <= 0 || K <= 0 || K > 1024 || C > (1 << 24)) return fail(LTHC_ERR_INVALID, fn, "C or K out of range");
+  if (!valid_dtype(a_dtype) || !valid_dtype(b_dtype) || !valid_dtype(out_dtype))
+    return fail(LTHC_ERR_INVALID, fn, "unknown dtype code");
+  if (grad == nullptr || alpha == nullptr || beta == nullptr) return fail(LTHC_ERR_INVALID, fn, "a NULL pointer");
+  PtrPack bp, gp;
+  for (int l = 0; l < L; ++l) {
+    if (beta[l] == nullptr) return fail(LTHC_ERR_INVALID, fn, "beta[" + std::to_string(l) + "] is NULL");
+    bp.p[l] = beta[l];
+    gp.p[l] = gbeta == nullptr ? nullptr : gbeta[l];
+  }
+  const int64_t n = C * K;
+  dispatch_dtype(out_dtype, [&](auto d) {
+    gamma_rounded_bwd_kernel<decltype(d)::value><<<static_cast<unsigned>((n + 255) / 256), 256, 0,
+                                                   static_cast<hipStream_t>(stream)>>>(
+        grad, alpha, a_dtype, bp, b_dtype, galpha, gp, static_cast<int>(C), static_cast<int>(K), L);
+  });
+  return check_launch(fn);
+}
+
 int lthc_recur_fwd(const void* z, const void* dz, int x_dtype, const void* gamma, int g_dtype, void* z_next,
                    int64_t rows, int64_t C, void* stream) {
   static const char* fn = "lthc_recur_fwd";
@@ -1717,6 +1788,49 @@ int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dty
       else
         recur_bwd_kernel<decltype(d)::value, typename decltype(o)::type, false>
             <<<grid, 256, 0, st>>>(g, dz, nullptr, gamma, g_dtype, gdz, partial, rows, static_cast<int>(C));
+    });
+  });
+  if (int rc = check_launch(fn)) return rc;
+  launch_reduce(partial, static_cast<int>(by * 4), C, ggamma, st);
+  return check_launch(fn);
+}
+
+int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, const void* gdz_add, int x_dtype,
+                       const void* gamma, int g_dtype, void* g_sum, void* gdz, float* ggamma, int64_t rows,
+                       int64_t C, void* workspace, size_t workspace_bytes, void* stream) {
+  static const char* fn = "lthc_recur_bwd_sum";
+  g_last_error.clear();
+  if (rows < 0 || C <= 0 || C % 4 != 0 || C > (1 << 24)) return fail(LTHC_ERR_INVALID, fn, "rows >= 0 and C > 0, C % 4 == 0 required");
+  if (!valid_dtype(x_dtype) || !valid_dtype(g_dtype)) return fail(LTHC_ERR_INVALID, fn, "unknown dtype code");
+  if (ggamma == nullptr || gamma == nullptr) return fail(LTHC_ERR_INVALID, fn, "gamma or ggamma is NULL");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  if (rows == 0) {
+    zero_kernel<<<static_cast<unsigned>((C + 255) / 256), 256, 0, st>>>(ggamma, C);
+    return check_launch(fn);
+  }
+  if (int rc = check_act(fn, g, x_dtype, "g")) return rc;
+  if (int rc = check_act(fn, g_branch, x_dtype, "g_branch")) return rc;
+  if (int rc = check_act(fn, dz, x_dtype, "dz")) return rc;
+  if (int rc = check_act(fn, g_sum, x_dtype, "g_sum")) return rc;
+  if (int rc = check_act(fn, gdz, x_dtype, "gdz")) return rc;
+  if (gdz_add != nullptr)
+    if (int rc = check_act(fn, gdz_add, x_dtype, "gdz_add")) return rc;
+  const size_t need = lthc_recur_bwd_workspace_bytes(rows, C);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(LTHC_ERR_INVALID, fn, "workspace smaller than lthc_recur_bwd_workspace_bytes()");
+  if (!aligned(workspace, 16)) return fail(LTHC_ERR_INVALID, fn, "workspace is not 16-byte aligned");
+  const int64_t by = recur_bwd_blocks_y(rows);
+  const dim3 grid(static_cast<unsigned>((C / 4 + 63) / 64), static_cast<unsigned>(by));
+  float* partial = static_cast<float*>(workspace);
+  const bool off32 = fits32(rows * C * esize(x_dtype));
+  dispatch_dtype(x_dtype, [&](auto d) {
+    dispatch_off(off32, [&](auto o) {
+      if (gdz_add != nullptr)
+        recur_bwd_kernel<decltype(d)::value, typename decltype(o)::type, true, true><<<grid, 256, 0, st>>>(
+            g, dz, gdz_add, gamma, g_dtype, gdz, partial, rows, static_cast<int>(C), g_branch, g_sum);
+      else
+        recur_bwd_kernel<decltype(d)::value, typename decltype(o)::type, false, true><<<grid, 256, 0, st>>>(
+            g, dz, nullptr, gamma, g_dtype, gdz, partial, rows, static_cast<int>(C), g_branch, g_sum);
     });
   });
   if (int rc = check_launch(fn)) return rc;

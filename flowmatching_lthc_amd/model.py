@@ -386,14 +386,21 @@ class SharedReadLocalTHCSharedAdaLNJiTBlock(nn.Module):
         return ops.lazy_workspace_update(z, dz, gamma)
 
     def lazy_workspace_step(
-        self, z: torch.Tensor, dz: torch.Tensor, shared_read: SharedLocalRead, gamma: torch.Tensor | None = None
-    ) -> tuple[torch.Tensor, torch.Tensor]:
+        self,
+        z: torch.Tensor,
+        dz: torch.Tensor,
+        shared_read: SharedLocalRead,
+        gamma: torch.Tensor | None = None,
+        split: bool = False,
+    ) -> tuple[torch.Tensor, ...]:
         """(lazy_workspace_update(z, dz), dz) for the lazy forward, where dz is also materialised at the end;
         the backward writes dz's whole gradient in one recurrence-backward pass (ops.lazy_workspace_step).
-        gamma: this layer's gamma_from_alpha(shared_read.alpha(dz.dtype)) when the caller has computed it."""
+        gamma: this layer's gamma_from_alpha(shared_read.alpha(dz.dtype)) when the caller has computed it.
+        split: return (z_next, z_next for the next block's branch, dz), whose backward also sums z_next's
+        two gradients in that pass."""
         if gamma is None:
             gamma = self.write.gamma_from_alpha(shared_read.alpha(dtype=dz.dtype))
-        return ops.lazy_workspace_step(z, dz, gamma)
+        return ops.lazy_workspace_step(z, dz, gamma, split)
 
 
 def migrate_lthc_state_dict_keys(state_dict: dict) -> dict:
@@ -557,18 +564,20 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
     def forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         t6, t2 = self._conditioning(t, y)
         # local_thc.py:1376-1385 (read once, one branch + recurrence per block, one materialisation).  The read
-        # and the recurrence steps are the fused-backward forms: same values, x0's and each dZ_l's gradient
-        # from one kernel instead of a kernel plus autograd's add.
+        # and the recurrence steps are the fused-backward forms: same values, x0's, each dZ_l's and each Z_l's
+        # gradient from one kernel instead of a kernel plus autograd's add.
         x0, z = self.shared_read.read_with_residual(self.x_embedder(x))
+        zb = z  # the next branch's input: z itself, or the step's branch output (same values)
         dz_list, gammas = [], None
         for i, block in enumerate(self.blocks):
-            dz = block.branch_update(z, t6, self.workspace_rope)
+            dz = block.branch_update(zb, t6, self.workspace_rope)
             if i == 0:
                 gammas = self._all_gammas(dz)
             if gammas is None:  # the reference's hook signature
                 z, dz = block.lazy_workspace_step(z, dz, self.shared_read)
+                zb = z
             else:
-                z, dz = block.lazy_workspace_step(z, dz, self.shared_read, gammas[i])
+                z, zb, dz = block.lazy_workspace_step(z, dz, self.shared_read, gammas[i], split=True)
             dz_list.append(dz)
         return self._decode(self.final_accumulate_reference(x0, dz_list), t2)
 

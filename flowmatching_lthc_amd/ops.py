@@ -776,6 +776,43 @@ def _(grad: Tensor, dz: Tensor, gamma: Tensor, gdz_add: Tensor | None = None):
     return torch.empty_like(grad), grad.new_empty((grad.shape[-1],), dtype=torch.float32)
 
 
+@torch.library.custom_op("jit_thc::lazy_workspace_update_backward_sum", mutates_args=())
+def lazy_workspace_update_backward_sum(
+    grad: Tensor, grad_branch: Tensor, dz: Tensor, gamma: Tensor, gdz_add: Tensor | None = None
+) -> tuple[Tensor, Tensor, Tensor]:
+    """(g = grad + grad_branch rounded to grad.dtype, gamma * g [+ gdz_add], fp32 [C] sum over rows of g * dz):
+    lazy_workspace_update_backward of the two gradients of z_next, summed in the same pass."""
+    _on_gpu(grad, grad_branch, dz, gamma)
+    c = _check_recur(grad, dz, gamma)
+    if grad_branch.shape != grad.shape:
+        raise ValueError(f"grad_branch {tuple(grad_branch.shape)} must match grad {tuple(grad.shape)}")
+    grad = _prep(grad)
+    dz, grad_branch = _same_dtype(grad, [_prep(dz), _prep(grad_branch)])
+    if gdz_add is not None:
+        if gdz_add.shape != grad.shape:
+            raise ValueError(f"gdz_add {tuple(gdz_add.shape)} must match grad {tuple(grad.shape)}")
+        (gdz_add,) = _same_dtype(grad, [_prep(gdz_add)])
+    gamma = _prep(gamma)
+    rows = grad.numel() // c
+    gsum = torch.empty_like(grad)
+    gdz = torch.empty_like(grad)
+    ggamma = torch.empty((c,), device=grad.device, dtype=torch.float32)
+    ws = torch.empty((max(_abi.recur_bwd_workspace_bytes(rows, c), 16),), device=grad.device, dtype=torch.uint8)
+    with _on_device(grad):
+        rc = _abi.load().lthc_recur_bwd_sum(
+            grad.data_ptr(), grad_branch.data_ptr(), dz.data_ptr(), _abi.ptr(gdz_add), _abi.code(grad),
+            gamma.data_ptr(), _abi.code(gamma), gsum.data_ptr(), gdz.data_ptr(), ggamma.data_ptr(), rows, c,
+            ws.data_ptr(), ws.numel(), _abi.stream_of(grad),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_recur_bwd_sum")
+    return gsum, gdz, ggamma
+
+
+@lazy_workspace_update_backward_sum.register_fake
+def _(grad: Tensor, grad_branch: Tensor, dz: Tensor, gamma: Tensor, gdz_add: Tensor | None = None):
+    return torch.empty_like(grad), torch.empty_like(grad), grad.new_empty((grad.shape[-1],), dtype=torch.float32)
+
+
 def _setup_recur_ctx(ctx, inputs, output):
     _, dz, gamma = inputs
     ctx.save_for_backward(dz, gamma)
@@ -798,45 +835,59 @@ torch.library.register_autograd(lazy_workspace_update, _backward_recur, setup_co
 
 
 class _RecurStep(torch.autograd.Function):
-    """(Z_{l+1} = Z_l + gamma * dZ_l, dZ_l) as one autograd node.
+    """(Z_{l+1} = Z_l + gamma * dZ_l, dZ_l) as one autograd node, or (Z_{l+1}, Z_{l+1}', dZ_l) with `split`.
 
     In the lazy forward dZ_l feeds both the recurrence and the final
     materialisation, so autograd would add the two gradients of dZ_l in a
     separate pass; here the node receives both and one recurrence-backward
-    launch writes gamma * g + (materialisation's gradient).
+    launch writes gamma * g + (materialisation's gradient).  With `split`,
+    Z_{l+1} is returned twice, one for the next recurrence step and one for
+    the next block's branch: the node then also receives Z_{l+1}'s two
+    gradients apart and sums them in the same launch, where autograd would
+    add them in a pass of its own.
     """
 
     @staticmethod
-    def forward(ctx, z: Tensor, dz: Tensor, gamma: Tensor):
+    def forward(ctx, z: Tensor, dz: Tensor, gamma: Tensor, split: bool):
         zn = lazy_workspace_update(z, dz, gamma)
         ctx.save_for_backward(dz, gamma)
         ctx.z_dtype = z.dtype
+        ctx.split = split
         ctx.set_materialize_grads(False)  # an unused Z_{l+1} (the last step's) skips the recurrence backward
+        if split:
+            return zn, zn.view_as(zn), dz.view_as(dz)
         return zn, dz.view_as(dz)
 
     @staticmethod
-    def backward(ctx, grad_zn: Tensor | None, grad_dz: Tensor | None):
+    def backward(ctx, *grads):
+        grad_zn, grad_branch, grad_dz = grads if ctx.split else (grads[0], None, grads[1])
         dz, gamma = ctx.saved_tensors
         need = ctx.needs_input_grad
         if grad_zn is None:
-            return None, grad_dz, None
-        grad_z = grad_zn.to(ctx.z_dtype) if need[0] else None
+            grad_zn, grad_branch = grad_branch, None
+        if grad_zn is None:
+            return None, grad_dz, None, None
         gdz = gg = None
-        if need[1] or need[2]:
-            add = grad_dz if need[1] else None
+        add = grad_dz if need[1] else None
+        if grad_branch is not None:
+            grad_zn, gdz, gg = lazy_workspace_update_backward_sum(grad_zn, grad_branch, dz, gamma, add)
+        elif need[1] or need[2]:
             gdz, gg = lazy_workspace_update_backward(grad_zn, dz, gamma, add)
-            gdz = gdz.to(dz.dtype) if need[1] else None
-            gg = gg.to(gamma.dtype) if need[2] else None
-        return grad_z, gdz, gg
+        grad_z = grad_zn.to(ctx.z_dtype) if need[0] else None
+        gdz = gdz.to(dz.dtype) if need[1] and gdz is not None else None
+        gg = gg.to(gamma.dtype) if need[2] and gg is not None else None
+        return grad_z, gdz, gg, None
 
 
-def lazy_workspace_step(z: Tensor, dz: Tensor, gamma: Tensor) -> tuple[Tensor, Tensor]:
+def lazy_workspace_step(z: Tensor, dz: Tensor, gamma: Tensor, split: bool = False) -> tuple[Tensor, ...]:
     """(lazy_workspace_update(z, dz, gamma), dz) with a fused backward for a later consumer of dz.
 
     Values are those of the separate uses; the backward of dz is gamma * g_next plus the later
     consumer's gradient, written by one recurrence-backward launch instead of a launch and an add.
+    split=True returns (z_next, z_next for the branch, dz): the same values, with z_next's two
+    gradients (next step, branch) summed by that launch too.
     """
-    return _RecurStep.apply(z, dz, gamma)
+    return _RecurStep.apply(z, dz, gamma, split)
 
 
 # ---------------------------------------------------------------------------
@@ -929,17 +980,28 @@ def _setup_gamma_rounded_ctx(ctx, inputs, output):
 
 
 def _backward_gamma_rounded(ctx, grad):
+    """Eager autograd's values for lazy_gamma_rounded_eager, from one lthc_gamma_rounded_bwd launch."""
     alpha, *betas = ctx.saved_tensors
     need_a, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-    with torch.enable_grad():
-        a = alpha.detach().requires_grad_(bool(need_a))
-        bs = [b.detach().requires_grad_(bool(need_b)) for b in betas]
-        out = lazy_gamma_rounded_eager(a, bs, ctx.dtype)
-        wanted = ([a] if need_a else []) + (bs if need_b else [])
-        got = list(torch.autograd.grad([out], wanted, [grad], allow_unused=True)) if wanted else []
-    ga = got.pop(0) if need_a else None
-    gb = got if need_b else None
-    return ga, gb, None
+    if not (need_a or need_b):
+        return None, None, None
+    bd = betas[0].dtype
+    betas = [b.contiguous() if b.dtype == bd else b.to(bd).contiguous() for b in betas]
+    alpha = alpha.contiguous()
+    grad = grad.to(ctx.dtype).contiguous()
+    ga = torch.empty_like(alpha) if need_a else None
+    gbs = [torch.empty_like(b) for b in betas] if need_b else None
+    c, k = alpha.shape
+    with _on_device(alpha):
+        rc = _abi.load().lthc_gamma_rounded_bwd(
+            grad.data_ptr(), alpha.data_ptr(), _abi.code(alpha), _abi.ptr_array(betas), _abi.code(betas[0]),
+            _abi.ptr(ga), _abi.ptr_array(gbs) if gbs is not None else None, _abi.code(grad), c, k, len(betas),
+            _abi.stream_of(alpha),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_gamma_rounded_bwd")
+    if gbs is not None:
+        gbs = [g if g.dtype == b.dtype else g.to(b.dtype) for g, b in zip(gbs, ctx.saved_tensors[1:])]
+    return ga, gbs, None
 
 
 torch.library.register_autograd(lazy_gamma_rounded, _backward_gamma_rounded, setup_context=_setup_gamma_rounded_ctx)

@@ -150,6 +150,20 @@ int lthc_gamma_rounded(const void* alpha, int a_dtype, const void* const* beta, 
                        int out_dtype, int64_t C, int64_t K, int L, void* stream);
 
 /*
+ * Backward of lthc_gamma_rounded: the values eager autograd gives for that
+ * sequence.  With a = r(alpha), b_l = r(beta_l), g_l = grad[l, c] (grad
+ * [L, C] in out_dtype):
+ *   gbeta_l[c,k] = r(g_l * a[c,k])                     written in b_dtype
+ *   galpha[c,k]  = the L products r(g_l * b_l[c,k]) summed in out_dtype,
+ *                  last layer first, each partial sum rounded (the order
+ *                  autograd accumulates a's gradient in)   written in a_dtype
+ * galpha may be NULL; gbeta may be NULL or hold NULL entries (no output).
+ */
+int lthc_gamma_rounded_bwd(const void* grad, const void* alpha, int a_dtype, const void* const* beta, int b_dtype,
+                           void* galpha, void* const* gbeta, int out_dtype, int64_t C, int64_t K, int L,
+                           void* stream);
+
+/*
  * LAZY WORKSPACE RECURRENCE STEP   z_next[r,c] = z[r,c] + gamma[c] * dz[r,c]
  * Replaces SharedReadLocalTHCSharedAdaLNJiTBlock.lazy_workspace_update
  * (local_thc.py:1325-1328); rows = B*M.  Computed as fma(gamma, dz, z).
@@ -171,6 +185,21 @@ size_t lthc_recur_bwd_workspace_bytes(int64_t rows, int64_t C);
 int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dtype, const void* gamma,
                    int g_dtype, void* gdz, float* ggamma, int64_t rows, int64_t C,
                    void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * RECURRENCE BACKWARD WITH THE BRANCH GRADIENT
+ *   g_sum[r,c] = g[r,c] + g_branch[r,c]                (x_dtype; one rounding)
+ *   then lthc_recur_bwd with g_sum in place of g.
+ * z_next feeds two consumers in the lazy forward, the next recurrence step
+ * and the next block's branch (local_thc.py:1383-1385); eager autograd adds
+ * their gradients in a separate pass before the recurrence backward of
+ * local_thc.py:1328 sees them.  Here the add happens in the same pass, with
+ * the same rounding, and g_sum (= dL/dz_next, which is also dL/dz) is
+ * written for the previous step.  Same workspace as lthc_recur_bwd.
+ */
+int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, const void* gdz_add, int x_dtype,
+                       const void* gamma, int g_dtype, void* g_sum, void* gdz, float* ggamma, int64_t rows,
+                       int64_t C, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * WORKSPACE ACCUMULATION (non-shared / triangular lazy interface)

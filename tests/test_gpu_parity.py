@@ -144,13 +144,15 @@ def test_config3_read_backward_bf16(coracle):
     assert_f32(host(da), coracle.Cweight_grad(host(x0), [host(gz)], G)[0], tol=1e-5, what="dalpha")
 
 
-@pytest.mark.parametrize("fused_open", [False, True])
+@pytest.mark.parametrize("fused_open", [False, True, "split"])
 def test_interface_autograd_matches_closed_form_fp32(coracle, fused_open):
     """Read op -> 4 recurrence ops -> stacked materialise op, backward through torch autograd.
 
     fused_open: the model's forward_lazy form -- the read and the materialisation's use of X0 go through
     ops.read_with_residual (dX0 = G_L + R^T gZ0 in one local_read_add pass) and every recurrence step
-    through ops.lazy_workspace_step (dZ_l's two gradients summed inside the recurrence backward)."""
+    through ops.lazy_workspace_step (dZ_l's two gradients summed inside the recurrence backward);
+    "split" also takes Z_l for the upstream gradient from the step's branch output (Z_l's two gradients
+    summed inside the recurrence backward)."""
     B, G, C, L = 2, 16, 64, 4
     d = cfg(B, G, C, L, seed=3, grads=True)
     t = lambda a: dev(a).requires_grad_(True)  # noqa: E731
@@ -163,11 +165,15 @@ def test_interface_autograd_matches_closed_form_fp32(coracle, fused_open):
     zs, dzm = [z], []
     for l in range(L):
         gam = (alpha * betas[l]).sum(-1)
-        if fused_open:
+        if fused_open == "split":
+            z, zb, dz_m = ops.lazy_workspace_step(z, dzs[l], gam, split=True)
+        elif fused_open:
             z, dz_m = ops.lazy_workspace_step(z, dzs[l], gam)
+            zb = z
         else:
             z, dz_m = ops.lazy_workspace_update(z, dzs[l], gam), dzs[l]
-        zs.append(z)
+            zb = z
+        zs.append(zb)
         dzm.append(dz_m)
     xl = ops.final_accumulate_b4_traceable(x0, torch.stack(dzm), betas)
     loss = (xl * dev(d["grad_xl"])).sum() + sum((zs[l] * dev(d["grad_z"][l])).sum() for l in range(L))
@@ -240,6 +246,63 @@ def test_recurrence_backward(coracle):
     gdz2, gg2 = capi.recur_bwd(g, dz, gam, add)
     assert_bf16(host(gdz2), rgdz.astype(np.float64) + host(add), what="gamma * g + add")
     assert torch.equal(gg2, gg)
+
+
+@pytest.mark.parametrize("xdt", [F32, BF16, torch.float16])
+@pytest.mark.parametrize("with_add", [False, True])
+@pytest.mark.parametrize("rows_c", [(8 * 256, 768), (3, 12), (1000, 260)])
+def test_recurrence_backward_with_branch_gradient(coracle, xdt, with_add, rows_c):
+    """lthc_recur_bwd_sum: g + g_branch rounded as autograd's add, then the recurrence backward of that sum --
+    bitwise equal to the add followed by lthc_recur_bwd, and the sum's backward against the oracle."""
+    rows, c = rows_c
+    gen = torch.Generator().manual_seed(rows + c)
+    mk = lambda s: dev(torch.randn((rows, c), generator=gen) * s, xdt)  # noqa: E731
+    g, gb, dz, add = mk(1e-3), mk(1e-3), mk(0.02), (mk(1e-3) if with_add else None)
+    gam = dev(torch.randn((c,), generator=gen) * 0.05)
+    gsum, gdz, gg = capi.recur_bwd_sum(g, gb, dz, gam, add)
+    assert torch.equal(gsum, g + gb), "g_sum differs from autograd's add"
+    gdz_ref, gg_ref = capi.recur_bwd(g + gb, dz, gam, add)
+    assert torch.equal(gdz, gdz_ref) and torch.equal(gg, gg_ref), "summed form differs from add + recurrence backward"
+    rgdz, rgg = coracle.Crecur_bwd(host(g + gb), host(dz), host(gam))
+    if add is not None:
+        rgdz = rgdz.astype(np.float64) + host(add)
+    if xdt == F32:
+        assert_f32(host(gdz), rgdz, what="gamma * (g + g_branch)")
+    else:
+        assert np.abs(host(gdz) - rgdz).max() <= 2e-2 * max(1.0, np.abs(rgdz).max())
+    assert_f32(host(gg), rgg, tol=1e-5, what="ggamma")
+
+
+def test_split_steps_gradients_equal_unsplit_bf16():
+    """ops.lazy_workspace_step(split=True): the branch reads the step's second output and the backward sums
+    z_next's two gradients inside the recurrence backward.  Every gradient is bitwise that of the unsplit form,
+    where autograd adds them (bf16, 6 steps, the last step's z_next unused as in forward_lazy)."""
+    B, G, C, L = 4, 16, 768, 6
+    gen = torch.Generator().manual_seed(11)
+    r = lambda *s, sc=1.0: (torch.randn(s, generator=gen) * sc)  # noqa: E731
+    z0 = dev(r(B, G * G, C), BF16)
+    dzs = [dev(r(B, G * G, C, sc=0.02), BF16) for _ in range(L)]
+    gam = dev(r(L, C, sc=0.05))
+    H = [dev(r(B, G * G, C, sc=1e-3), BF16) for _ in range(L)]
+    gm = dev(r(B, G * G, C, sc=1e-3), BF16)
+
+    def grads(split):
+        leaves = [t.clone().requires_grad_(True) for t in [z0, gam] + dzs]
+        z, gm_ = leaves[0], leaves[1]
+        zb, zs, dl = z, [], []
+        for l in range(L):
+            zs.append(zb)
+            if split:
+                z, zb, d = ops.lazy_workspace_step(z, leaves[2 + l], gm_[l], split=True)
+            else:
+                z, d = ops.lazy_workspace_step(z, leaves[2 + l], gm_[l])
+                zb = z
+            dl.append(d)
+        out = torch.stack(dl).sum(0)  # a consumer of every dz, as the materialisation
+        return torch.autograd.grad([out] + zs, leaves, [gm] + H)
+
+    for a, b in zip(grads(True), grads(False)):
+        assert torch.equal(a, b)
 
 
 # ---------------------------------------------------------------------------
