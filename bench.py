@@ -425,7 +425,7 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
 
     X0, alpha, the 12 beta_l and the 12 dZ_l are leaves that require grad; the upstream gradients are
     G_L = dL/dX_L ~ N(0, 1e-3) and H_l = dL/dZ_l ~ N(0, 1e-3) for the 12 workspace states Z_0..Z_11 that feed
-    the branches.  One step = read (the fused-open form of the model's forward_lazy), gamma stack, 12
+    the branches.  One step = read (the fused-open form of the model's forward_lazy), every gamma (one launch), 12
     recurrence steps, 12-pointer materialise, then torch.autograd.grad over (X_L, Z_0..Z_11) -- every backward
     kernel of the interface plus autograd's own gradient accumulation (adds), as in training."""
     B = args.train_batch if B is None else B
@@ -445,8 +445,9 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
 
     def forward():
         x0v, z = ops.read_with_residual(x0, alpha.to(bf16))  # as the model's forward_lazy
-        # gamma rows as one unbind (its backward is one stack, not a zero-fill + copy + add per layer)
-        gam = ops.lazy_gamma_stack(alpha.to(bf16), torch.stack([b.to(bf16) for b in betas])).unbind(0)
+        # every layer's gamma_from_alpha in one launch, as the model's forward_lazy; the rows as one unbind (its
+        # backward is one stack, not a zero-fill + copy + add per layer)
+        gam = ops.lazy_gamma_rounded(alpha, betas, bf16).unbind(0)
         zs, dzv = [z], []
         for l in range(L):
             z, zb, d = ops.lazy_workspace_step(z, dzs[l], gam[l], split=True)  # as the model's forward_lazy

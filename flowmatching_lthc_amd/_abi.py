@@ -87,7 +87,7 @@ def load() -> ctypes.CDLL:
         "lthc_gamma_rounded_bwd": [vp, vp, ci, pp, ci, vp, pp, ci, i64, i64, ci, vp],
         "lthc_recur_fwd": [vp, vp, ci, vp, ci, vp, i64, i64, vp],
         "lthc_recur_bwd": [vp, vp, vp, ci, vp, ci, vp, vp, i64, i64, vp, sz, vp],
-        "lthc_recur_bwd_sum": [vp, vp, vp, vp, ci, vp, ci, vp, vp, vp, i64, i64, vp, sz, vp],
+        "lthc_recur_bwd_sum": [vp, vp, vp, vp, ci, vp, ci, vp, vp, vp, ci, i64, i64, vp, sz, vp],
         "lthc_ws_accumulate_fwd": [vp, pp, ci, vp, ci, vp, i64, i64, ci, vp],
         "lthc_ws_accumulate_bwd": [vp, pp, ci, vp, ci, pp, vp, i64, i64, ci, vp, sz, vp],
         "lthc_norm_modulate_fwd": [vp, ci, vp, ci, vp, vp, i64, vp, vp, i64, i64, i64, ctypes.c_float, vp],

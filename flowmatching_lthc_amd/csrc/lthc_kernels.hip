@@ -708,12 +708,15 @@ __global__ __launch_bounds__(kBlock) void cell_read_multi_kernel(const void* __r
 
 // ---------------------------------------------------------------------------
 // WHOLE-CELL CELL WEIGHT GRADIENT, stage 1 (depth <= 24, tensors below 4 GiB):
-//   partial[bx, l, c, k] = sum_{cells of block column bx} high[cell,k,c] low_l[cell,c]
+//   partial[bx, l, c, k] = sum_{cells of block bx} high[cell,k,c] low_l[cell,c]
 // Thread = CPT channels x the 16 / TG taps of its tap group (as
 // cell_mat_kernel); its LMAX x CPT x (16 / TG) fp32 accumulators stay in
-// VGPRs over the block column's grid-stride cells.  Every block writes its
-// partial slot, zeros included.  Padding layers accumulate layer 0 and are
-// never written.
+// VGPRs.  A block's four wavefronts are TG tap groups x WC = 4 / TG cell
+// lanes over the same 64 x CPT channels: cell lane w of block bx visits cells
+// bx * WC + w, + WC * gridDim.x, ...  At the end the WC cell lanes are added
+// in lane order through LDS, so each block writes one partial slot (zeros
+// included) -- WC times fewer partial bytes than a slot per wavefront.
+// Padding layers accumulate layer 0 and are never written.
 // ---------------------------------------------------------------------------
 template <int DT, int LMAX, int CPT, int TG>
 __global__ __launch_bounds__(kBlock) void cell_wgrad_kernel(const void* __restrict__ high, PtrPack low,
@@ -721,11 +724,18 @@ __global__ __launch_bounds__(kBlock) void cell_wgrad_kernel(const void* __restri
                                                             int C) {
   constexpr int ES = Fmt<DT>::bytes;
   constexpr int TPT = kK / TG;
-  constexpr int QL = kBlock / TG;
-  const int g = TG == 1 ? 0 : __builtin_amdgcn_readfirstlane(threadIdx.x / QL);  // wave-uniform tap group
-  const int c0 = (blockIdx.y * QL + (threadIdx.x - g * QL)) * CPT;
+  constexpr int WC = 4 / TG;                  // cell lanes per tap group
+  constexpr int PER = CPT * TPT;              // accumulators per layer
+  constexpr int LC = 64 / PER < 1 ? 1 : (64 / PER > LMAX ? LMAX : 64 / PER);  // layers per LDS round
+  constexpr int SLOTS = LC * PER / 4;         // float4 per lane per round
+  static_assert(PER % 4 == 0 && LMAX % LC == 0, "weight-gradient reduction rounds");
+  __shared__ float4 red[(WC - 1) * TG][SLOTS][64];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int g = w % TG, cw = w / TG;
+  const int c0 = (blockIdx.y * 64 + lane) * CPT;
   const int tap0 = g * TPT;
-  if (c0 >= C) return;
+  const bool active = c0 < C;  // every thread reaches the reduction's barriers
   float acc[LMAX][CPT][TPT];
 #pragma unroll
   for (int l = 0; l < LMAX; ++l)
@@ -735,11 +745,11 @@ __global__ __launch_bounds__(kBlock) void cell_wgrad_kernel(const void* __restri
       for (int k = 0; k < TPT; ++k) acc[l][v][k] = 0.f;
   const uint32_t tap_b = C * ES;
   const uint32_t row_b = G * kS * tap_b;
-  const uint32_t P = gridDim.x;
+  const uint32_t P = gridDim.x * WC;  // cell stride, a multiple of G
   const uint32_t step_x = (P / G) * kS * row_b;
   const uint32_t step_z = P * tap_b;
-  uint32_t cell = blockIdx.x;
-  uint32_t ho = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES) + (tap0 / kS) * row_b;
+  uint32_t cell = active ? blockIdx.x * WC + cw : ncells;
+  uint32_t ho = static_cast<uint32_t>((cell_hoff(cell < ncells ? cell : 0, G, C) + c0) * ES) + (tap0 / kS) * row_b;
   uint32_t zo = (cell * C + c0) * ES;
   for (; cell < ncells; cell += P, ho += step_x, zo += step_z) {
     Raw<DT, CPT> hr[TPT];
@@ -764,16 +774,34 @@ __global__ __launch_bounds__(kBlock) void cell_wgrad_kernel(const void* __restri
   }
   float* dst = partial + static_cast<int64_t>(blockIdx.x) * L * C * kK;
 #pragma unroll
-  for (int l = 0; l < LMAX; ++l) {
-    if (l < L) {
+  for (int l0 = 0; l0 < LMAX; l0 += LC) {
+    if (cw > 0) {
 #pragma unroll
-      for (int v = 0; v < CPT; ++v) {
-        float4* row = reinterpret_cast<float4*>(dst + (static_cast<int64_t>(l) * C + c0 + v) * kK + tap0);
-#pragma unroll
-        for (int q = 0; q < TPT / 4; ++q)
-          row[q] = make_float4(acc[l][v][4 * q], acc[l][v][4 * q + 1], acc[l][v][4 * q + 2], acc[l][v][4 * q + 3]);
+      for (int q = 0; q < SLOTS; ++q) {
+        const int e = 4 * q;  // element e of the round: layer l0 + e / PER, channel (e % PER) / TPT, taps e % TPT + 0..3
+        const int l = l0 + e / PER, v = (e % PER) / TPT, k = e % TPT;
+        red[(cw - 1) * TG + g][q][lane] = make_float4(acc[l][v][k], acc[l][v][k + 1], acc[l][v][k + 2], acc[l][v][k + 3]);
       }
     }
+    __syncthreads();
+    if (cw == 0 && active) {
+#pragma unroll
+      for (int q = 0; q < SLOTS; ++q) {
+        const int e = 4 * q;
+        const int l = l0 + e / PER, v = (e % PER) / TPT, k = e % TPT;
+        float4 t = make_float4(acc[l][v][k], acc[l][v][k + 1], acc[l][v][k + 2], acc[l][v][k + 3]);
+#pragma unroll
+        for (int r = 1; r < WC; ++r) {
+          const float4 b = red[(r - 1) * TG + g][q][lane];
+          t.x += b.x;
+          t.y += b.y;
+          t.z += b.z;
+          t.w += b.w;
+        }
+        if (l < L) *reinterpret_cast<float4*>(dst + (static_cast<int64_t>(l) * C + c0 + v) * kK + tap0 + k) = t;
+      }
+    }
+    __syncthreads();
   }
 }
 
@@ -782,14 +810,15 @@ __global__ __launch_bounds__(256) void zero_kernel(float* __restrict__ out, int6
   if (i < n) out[i] = 0.f;
 }
 
-// Stage 2: out[i] = sum_{p < nparts} partial[p, i] in ascending p.
+// Stage 2: out[i] = sum_{p < nparts} partial[p, i] in ascending p, stored in
+// format odt (the fp32 sum rounded once).
 __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __restrict__ partial, int nparts,
-                                                              int64_t n, float* __restrict__ out) {
+                                                              int64_t n, void* __restrict__ out, int odt) {
   const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
   if (i >= n) return;
   float s = 0.f;
   for (int p = 0; p < nparts; ++p) s += partial[static_cast<int64_t>(p) * n + i];
-  out[i] = s;
+  store_w(out, odt, i, s);
 }
 
 // Narrow outputs (few columns, many partial rows): block = 16 columns x 16
@@ -798,7 +827,7 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
 // is bitwise reproducible, with 16x the parallelism of reduce_partials_kernel.
 constexpr int kRedGroups = 16;
 __global__ __launch_bounds__(256) void reduce_partials_split_kernel(const float* __restrict__ partial, int nparts,
-                                                                    int64_t n, float* __restrict__ out) {
+                                                                    int64_t n, void* __restrict__ out, int odt) {
   __shared__ float part[kRedGroups][16];
   const int col = threadIdx.x & 15;
   const int grp = threadIdx.x >> 4;
@@ -822,7 +851,7 @@ __global__ __launch_bounds__(256) void reduce_partials_split_kernel(const float*
     float t = 0.f;
 #pragma unroll
     for (int g = 0; g < kRedGroups; ++g) t += part[g][col];
-    out[i] = t;
+    store_w(out, odt, i, t);
   }
 }
 
@@ -882,31 +911,75 @@ __global__ __launch_bounds__(256) void gamma_rounded_kernel(const void* __restri
   store_w(gamma, ODT, i, s);
 }
 
+// The same for K = 16 taps with 16-byte aligned rows: one vector load per row,
+// compile-time dtypes, the same rounding and summation order.
+template <int ODT, int ADT, int BDT>
+__global__ __launch_bounds__(256) void gamma16_rounded_kernel(const void* __restrict__ alpha, PtrPack beta,
+                                                              void* __restrict__ gamma, int C, int L) {
+#pragma clang fp contract(off)
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= static_cast<int64_t>(L) * C) return;
+  const int l = static_cast<int>(i / C);
+  const int c = static_cast<int>(i - static_cast<int64_t>(l) * C);
+  float a[kK], b[kK];
+  load_wvec<ADT, kK>(alpha, static_cast<int64_t>(c) * kK, a);
+  load_wvec<BDT, kK>(beta.p[l], static_cast<int64_t>(c) * kK, b);
+  float s = 0.f;
+#pragma unroll
+  for (int k = 0; k < kK; ++k) s += round_w<ODT>(round_w<ODT>(a[k]) * round_w<ODT>(b[k]));
+  store_w(gamma, ODT, i, s);
+}
+
 // Its backward, the eager autograd of that sequence: with a = r(alpha),
 // b_l = r(beta_l) and g_l = grad[l, c],
 //   gbeta_l[c,k] = r(g_l * a[c,k])
 //   galpha[c,k]  = r(... r(r(g_{L-1} b_{L-1}) + r(g_{L-2} b_{L-2})) ... + r(g_0 b_0))
 // the L products being summed into a's gradient in the order autograd
 // delivers them (last layer first), each partial sum rounded.
-template <int ODT>
+// Blocks [0, nb_beta) write gbeta, one thread per (l, c, k); the blocks after
+// them write galpha, one thread per (c, k) over the L layers.
+template <int ODT, int BDT, int LMAX>
 __global__ __launch_bounds__(256) void gamma_rounded_bwd_kernel(const void* __restrict__ grad,
                                                                 const void* __restrict__ alpha, int adt,
-                                                                PtrPack beta, int bdt, void* __restrict__ galpha,
-                                                                PtrPack gbeta, int C, int K, int L) {
+                                                                PtrPack beta, void* __restrict__ galpha,
+                                                                PtrPack gbeta, int C, int K, int L, int nb_beta) {
 #pragma clang fp contract(off)
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  if (i >= static_cast<int64_t>(C) * K) return;
-  const int c = static_cast<int>(i / K);
-  const float a = round_w<ODT>(load_w(alpha, adt, i));
-  float acc = 0.f;
-  for (int l = L - 1; l >= 0; --l) {
-    const float g = load_w(grad, ODT, static_cast<int64_t>(l) * C + c);
-    const float b = round_w<ODT>(load_w(beta.p[l], bdt, i));
-    const float pa = round_w<ODT>(g * b);
-    acc = l == L - 1 ? pa : round_w<ODT>(acc + pa);
-    if (gbeta.p[l] != nullptr) store_w(const_cast<void*>(gbeta.p[l]), bdt, i, round_w<ODT>(g * a));
+  const int64_t n = static_cast<int64_t>(C) * K;
+  if (static_cast<int>(blockIdx.x) < nb_beta) {
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (j >= n * L) return;
+    const int l = static_cast<int>(j / n);
+    const int64_t i = j - l * n;
+    if (gbeta.p[l] == nullptr) return;
+    const float g = load_w(grad, ODT, static_cast<int64_t>(l) * C + i / K);
+    const float a = round_w<ODT>(load_w(alpha, adt, i));
+    store_w(const_cast<void*>(gbeta.p[l]), BDT, i, round_w<ODT>(g * a));
+    return;
   }
-  if (galpha != nullptr) store_w(galpha, adt, i, acc);
+  const int64_t i = static_cast<int64_t>(blockIdx.x - nb_beta) * 256 + threadIdx.x;
+  if (i >= n || galpha == nullptr) return;
+  const int c = static_cast<int>(i / K);
+  // every layer's loads first, unconditional so that they are in flight together (padding layers
+  // l >= L load layer 0 and are not used), then the products
+  float gv[LMAX], bv[LMAX];
+#pragma unroll
+  for (int l = 0; l < LMAX; ++l) {
+    const int ll = l < L ? l : 0;
+    float g1[1], b1[1];
+    load_wvec<ODT, 1>(grad, static_cast<int64_t>(ll) * C + c, g1);
+    load_wvec<BDT, 1>(beta.p[ll], i, b1);
+    gv[l] = g1[0];
+    bv[l] = round_w<ODT>(b1[0]);
+  }
+  float acc = 0.f;
+#pragma unroll
+  for (int l = LMAX - 1; l >= 0; --l) {
+    if (l < L) {
+      const float pa = round_w<ODT>(gv[l] * bv[l]);
+      acc = l == L - 1 ? pa : round_w<ODT>(acc + pa);
+    }
+  }
+  store_w(galpha, adt, i, acc);
 }
 
 // ---------------------------------------------------------------------------
@@ -985,9 +1058,10 @@ __global__ __launch_bounds__(256) void recur_fwd_flat_kernel(const void* __restr
   store_at<DT, VEC>(zn, off, a);
 }
 
-// RECURRENCE BACKWARD: gdz = gamma * g (+ gadd, HAS_ADD); partial[4*by + lane_row, c]
-// = sum g*dz over the rows the thread visits.  Grid and row order as
-// recur_fwd_kernel.  HAS_G2: g is the sum of two gradients, g + g2 rounded to
+// RECURRENCE BACKWARD: gdz = gamma * g (+ gadd, HAS_ADD); partial[by, c] = sum
+// g*dz over the rows the block visits (each thread's rows summed in its
+// order, then the block's 4 row lanes added in lane order).  Grid and row
+// order as recur_fwd_kernel.  HAS_G2: g is the sum of two gradients, g + g2 rounded to
 // DT (the value of autograd's add of the two), which is also written to gsum.
 template <int DT, typename Off, bool HAS_ADD, bool HAS_G2 = false>
 __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__ g, const void* __restrict__ dz,
@@ -999,12 +1073,14 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
   constexpr int ES = Fmt<DT>::bytes;
   const int t = threadIdx.x;
   const int c0 = (blockIdx.x * 64 + (t & 63)) * 4;
-  if (c0 >= C) return;
-  float gm[4];
+  const bool active = c0 < C;  // every thread reaches the block reduction below
+  float gm[4] = {0.f, 0.f, 0.f, 0.f};
+  if (active) {
 #pragma unroll
-  for (int v = 0; v < 4; ++v) gm[v] = load_w(gamma, gdt, c0 + v);
+    for (int v = 0; v < 4; ++v) gm[v] = load_w(gamma, gdt, c0 + v);
+  }
   float s[4] = {0.f, 0.f, 0.f, 0.f};
-  const int64_t re = rows;
+  const int64_t re = active ? rows : 0;
   const int64_t S = static_cast<int64_t>(4 * kRU) * gridDim.y;
   for (int64_t r0 = static_cast<int64_t>(blockIdx.y) * 4 * kRU + (t >> 6); r0 < re; r0 += S) {
     Raw<DT, 4> ar[kRU], dr[kRU], xr[HAS_ADD ? kRU : 1], br[HAS_G2 ? kRU : 1];
@@ -1055,8 +1131,21 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
       }
     }
   }
-  float* dst = partial + (static_cast<int64_t>(blockIdx.y) * 4 + (t >> 6)) * C + c0;
-  *reinterpret_cast<float4*>(dst) = make_float4(s[0], s[1], s[2], s[3]);
+  __shared__ float4 lane_sum[4][64];
+  lane_sum[t >> 6][t & 63] = make_float4(s[0], s[1], s[2], s[3]);
+  __syncthreads();
+  if (t < 64 && active) {
+    float4 a = lane_sum[0][t];
+#pragma unroll
+    for (int q = 1; q < 4; ++q) {
+      const float4 b = lane_sum[q][t];
+      a.x += b.x;
+      a.y += b.y;
+      a.z += b.z;
+      a.w += b.w;
+    }
+    *reinterpret_cast<float4*>(partial + static_cast<int64_t>(blockIdx.y) * C + c0) = a;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -1158,18 +1247,18 @@ int resident_blocks(K kernel) {
 
 // Recurrence forward: row chunks (of 4 * kRU rows) in flight per channel
 // block column, measured best at 1024 on MI355X.  Backward: 256 (each block
-// row leaves 4 partial rows of C floats to reduce).
+// row leaves one partial row of C floats to reduce).
 const int64_t kRecurChunks = 1024;
 const int64_t kRecurBwdChunks = 256;
 
 int64_t recur_bwd_blocks_y(int64_t rows) { return std::min((rows + 4 * kRU - 1) / (4 * kRU), kRecurBwdChunks); }
 
 // Deterministic reduction of nparts partial rows of n floats into out.
-void launch_reduce(const float* partial, int nparts, int64_t n, float* out, hipStream_t st) {
+void launch_reduce(const float* partial, int nparts, int64_t n, void* out, hipStream_t st, int odt = LTHC_F32) {
   if (nparts <= kRedGroups) {
-    reduce_partials_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(partial, nparts, n, out);
+    reduce_partials_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(partial, nparts, n, out, odt);
   } else {
-    reduce_partials_split_kernel<<<static_cast<unsigned>((n + 15) / 16), 256, 0, st>>>(partial, nparts, n, out);
+    reduce_partials_split_kernel<<<static_cast<unsigned>((n + 15) / 16), 256, 0, st>>>(partial, nparts, n, out, odt);
   }
 }
 
@@ -1233,9 +1322,13 @@ void wgrad_shape(int L, int& tpt, int& cpt);
 template <int DT, int LMAX>
 void cell_wgrad_plan_l(WgradPlan& p, int64_t ncells, int G, int64_t C) {
   constexpr int CPT = CellMatShape<DT, LMAX>::CPT, GR = CellMatShape<DT, LMAX>::GR;
+  constexpr int WC = 4 / GR;  // cell lanes per block: the cell stride nbx * WC must be a multiple of G
   static const int per_cu = resident_blocks(cell_wgrad_kernel<DT, LMAX, CPT, GR>);
-  p.slabs = static_cast<int>((C / CPT + kBlock / GR - 1) / (kBlock / GR));
-  p.nbx = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu / p.slabs, ncells, G, 1);
+  p.slabs = static_cast<int>((C / CPT + 63) / 64);
+  const int64_t unit = G / std::gcd<int64_t>(G, WC);
+  const int64_t want = static_cast<int64_t>(num_cus()) * per_cu / p.slabs;
+  const int64_t cap = ((ncells + WC - 1) / WC + unit - 1) / unit * unit;
+  p.nbx = std::max<int64_t>(unit, std::min<int64_t>(want / unit * unit, cap));
 }
 
 WgradPlan wgrad_plan(int dt, int64_t ncells, int G, int64_t C, int L, int blocks_per_cu = 2) {
@@ -1680,10 +1773,24 @@ int lthc_gamma_rounded(const void* alpha, int a_dtype, const void* const* beta, 
     bp.p[l] = beta[l];
   }
   const int64_t n = static_cast<int64_t>(L) * C;
+  const unsigned blocks = static_cast<unsigned>((n + 255) / 256);
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  bool rows16 = K == kK && aligned(alpha, 16);
+  for (int l = 0; l < L; ++l) rows16 = rows16 && aligned(beta[l], 16);
+  if (rows16) {
+    dispatch_dtype(out_dtype, [&](auto d) {
+      dispatch_dtype(a_dtype, [&](auto ad) {
+        dispatch_dtype(b_dtype, [&](auto bd) {
+          gamma16_rounded_kernel<decltype(d)::value, decltype(ad)::value, decltype(bd)::value>
+              <<<blocks, 256, 0, st>>>(alpha, bp, gamma, static_cast<int>(C), L);
+        });
+      });
+    });
+    return check_launch(fn);
+  }
   dispatch_dtype(out_dtype, [&](auto d) {
-    gamma_rounded_kernel<decltype(d)::value><<<static_cast<unsigned>((n + 255) / 256), 256, 0,
-                                               static_cast<hipStream_t>(stream)>>>(
-        alpha, a_dtype, bp, b_dtype, gamma, static_cast<int>(C), static_cast<int>(K), L);
+    gamma_rounded_kernel<decltype(d)::value><<<blocks, 256, 0, st>>>(alpha, a_dtype, bp, b_dtype, gamma,
+                                                                     static_cast<int>(C), static_cast<int>(K), L);
   });
   return check_launch(fn);
 }
@@ -1705,10 +1812,19 @@ int lthc_gamma_rounded_bwd(const void* grad, const void* alpha, int a_dtype, con
     gp.p[l] = gbeta == nullptr ? nullptr : gbeta[l];
   }
   const int64_t n = C * K;
+  const int64_t nb_beta = gbeta == nullptr ? 0 : (n * L + 255) / 256;
+  const int64_t nb_alpha = galpha == nullptr ? 0 : (n + 255) / 256;
+  if (nb_beta + nb_alpha == 0) return LTHC_OK;
   dispatch_dtype(out_dtype, [&](auto d) {
-    gamma_rounded_bwd_kernel<decltype(d)::value><<<static_cast<unsigned>((n + 255) / 256), 256, 0,
-                                                   static_cast<hipStream_t>(stream)>>>(
-        grad, alpha, a_dtype, bp, b_dtype, galpha, gp, static_cast<int>(C), static_cast<int>(K), L);
+    dispatch_dtype(b_dtype, [&](auto bd) {
+      constexpr int ODT = decltype(d)::value, BDT = decltype(bd)::value;
+      const auto kernel = L <= 12   ? gamma_rounded_bwd_kernel<ODT, BDT, 12>
+                          : L <= 24 ? gamma_rounded_bwd_kernel<ODT, BDT, 24>
+                                    : gamma_rounded_bwd_kernel<ODT, BDT, LTHC_MAX_LAYERS>;
+      kernel<<<static_cast<unsigned>(nb_beta + nb_alpha), 256, 0, static_cast<hipStream_t>(stream)>>>(
+          grad, alpha, a_dtype, bp, galpha, gp, static_cast<int>(C), static_cast<int>(K), L,
+          static_cast<int>(nb_beta));
+    });
   });
   return check_launch(fn);
 }
@@ -1751,7 +1867,7 @@ int lthc_recur_fwd(const void* z, const void* dz, int x_dtype, const void* gamma
 
 size_t lthc_recur_bwd_workspace_bytes(int64_t rows, int64_t C) {
   if (rows <= 0 || C <= 0) return 0;
-  return static_cast<size_t>(recur_bwd_blocks_y(rows) * 4 * C) * sizeof(float);
+  return static_cast<size_t>(recur_bwd_blocks_y(rows) * C) * sizeof(float);
 }
 
 int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dtype, const void* gamma, int g_dtype,
@@ -1791,21 +1907,22 @@ int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dty
     });
   });
   if (int rc = check_launch(fn)) return rc;
-  launch_reduce(partial, static_cast<int>(by * 4), C, ggamma, st);
+  launch_reduce(partial, static_cast<int>(by), C, ggamma, st);
   return check_launch(fn);
 }
 
 int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, const void* gdz_add, int x_dtype,
-                       const void* gamma, int g_dtype, void* g_sum, void* gdz, float* ggamma, int64_t rows,
-                       int64_t C, void* workspace, size_t workspace_bytes, void* stream) {
+                       const void* gamma, int g_dtype, void* g_sum, void* gdz, void* ggamma, int gg_dtype,
+                       int64_t rows, int64_t C, void* workspace, size_t workspace_bytes, void* stream) {
   static const char* fn = "lthc_recur_bwd_sum";
   g_last_error.clear();
   if (rows < 0 || C <= 0 || C % 4 != 0 || C > (1 << 24)) return fail(LTHC_ERR_INVALID, fn, "rows >= 0 and C > 0, C % 4 == 0 required");
-  if (!valid_dtype(x_dtype) || !valid_dtype(g_dtype)) return fail(LTHC_ERR_INVALID, fn, "unknown dtype code");
+  if (!valid_dtype(x_dtype) || !valid_dtype(g_dtype) || !valid_dtype(gg_dtype))
+    return fail(LTHC_ERR_INVALID, fn, "unknown dtype code");
   if (ggamma == nullptr || gamma == nullptr) return fail(LTHC_ERR_INVALID, fn, "gamma or ggamma is NULL");
   const hipStream_t st = static_cast<hipStream_t>(stream);
   if (rows == 0) {
-    zero_kernel<<<static_cast<unsigned>((C + 255) / 256), 256, 0, st>>>(ggamma, C);
+    launch_reduce(nullptr, 0, C, ggamma, st, gg_dtype);  // no parts: zeros
     return check_launch(fn);
   }
   if (int rc = check_act(fn, g, x_dtype, "g")) return rc;
@@ -1834,7 +1951,7 @@ int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, cons
     });
   });
   if (int rc = check_launch(fn)) return rc;
-  launch_reduce(partial, static_cast<int>(by * 4), C, ggamma, st);
+  launch_reduce(partial, static_cast<int>(by), C, ggamma, st, gg_dtype);
   return check_launch(fn);
 }
 

@@ -780,8 +780,9 @@ def _(grad: Tensor, dz: Tensor, gamma: Tensor, gdz_add: Tensor | None = None):
 def lazy_workspace_update_backward_sum(
     grad: Tensor, grad_branch: Tensor, dz: Tensor, gamma: Tensor, gdz_add: Tensor | None = None
 ) -> tuple[Tensor, Tensor, Tensor]:
-    """(g = grad + grad_branch rounded to grad.dtype, gamma * g [+ gdz_add], fp32 [C] sum over rows of g * dz):
-    lazy_workspace_update_backward of the two gradients of z_next, summed in the same pass."""
+    """(g = grad + grad_branch rounded to grad.dtype, gamma * g [+ gdz_add], [C] sum over rows of g * dz in fp32,
+    rounded once to gamma's dtype): lazy_workspace_update_backward of the two gradients of z_next, summed in the
+    same pass."""
     _on_gpu(grad, grad_branch, dz, gamma)
     c = _check_recur(grad, dz, gamma)
     if grad_branch.shape != grad.shape:
@@ -796,13 +797,13 @@ def lazy_workspace_update_backward_sum(
     rows = grad.numel() // c
     gsum = torch.empty_like(grad)
     gdz = torch.empty_like(grad)
-    ggamma = torch.empty((c,), device=grad.device, dtype=torch.float32)
+    ggamma = torch.empty((c,), device=grad.device, dtype=gamma.dtype)
     ws = torch.empty((max(_abi.recur_bwd_workspace_bytes(rows, c), 16),), device=grad.device, dtype=torch.uint8)
     with _on_device(grad):
         rc = _abi.load().lthc_recur_bwd_sum(
             grad.data_ptr(), grad_branch.data_ptr(), dz.data_ptr(), _abi.ptr(gdz_add), _abi.code(grad),
-            gamma.data_ptr(), _abi.code(gamma), gsum.data_ptr(), gdz.data_ptr(), ggamma.data_ptr(), rows, c,
-            ws.data_ptr(), ws.numel(), _abi.stream_of(grad),
+            gamma.data_ptr(), _abi.code(gamma), gsum.data_ptr(), gdz.data_ptr(), ggamma.data_ptr(), _abi.code(ggamma),
+            rows, c, ws.data_ptr(), ws.numel(), _abi.stream_of(grad),
         )  # fmt: skip
     _abi.check(rc, "lthc_recur_bwd_sum")
     return gsum, gdz, ggamma
@@ -810,7 +811,7 @@ def lazy_workspace_update_backward_sum(
 
 @lazy_workspace_update_backward_sum.register_fake
 def _(grad: Tensor, grad_branch: Tensor, dz: Tensor, gamma: Tensor, gdz_add: Tensor | None = None):
-    return torch.empty_like(grad), torch.empty_like(grad), grad.new_empty((grad.shape[-1],), dtype=torch.float32)
+    return torch.empty_like(grad), torch.empty_like(grad), grad.new_empty((grad.shape[-1],), dtype=gamma.dtype)
 
 
 def _setup_recur_ctx(ctx, inputs, output):

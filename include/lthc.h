@@ -195,11 +195,13 @@ int lthc_recur_bwd(const void* g, const void* dz, const void* gdz_add, int x_dty
  * their gradients in a separate pass before the recurrence backward of
  * local_thc.py:1328 sees them.  Here the add happens in the same pass, with
  * the same rounding, and g_sum (= dL/dz_next, which is also dL/dz) is
- * written for the previous step.  Same workspace as lthc_recur_bwd.
+ * written for the previous step.  ggamma is the fp32 sum rounded once to
+ * gg_dtype (gamma's own dtype saves the caller a cast).  Same workspace as
+ * lthc_recur_bwd.
  */
 int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, const void* gdz_add, int x_dtype,
-                       const void* gamma, int g_dtype, void* g_sum, void* gdz, float* ggamma, int64_t rows,
-                       int64_t C, void* workspace, size_t workspace_bytes, void* stream);
+                       const void* gamma, int g_dtype, void* g_sum, void* gdz, void* ggamma, int gg_dtype,
+                       int64_t rows, int64_t C, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * WORKSPACE ACCUMULATION (non-shared / triangular lazy interface)

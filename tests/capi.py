@@ -99,15 +99,18 @@ def recur_bwd(gr: torch.Tensor, dz: torch.Tensor, gam: torch.Tensor, add: torch.
     return gdz, gg
 
 
-def recur_bwd_sum(gr: torch.Tensor, gb: torch.Tensor, dz: torch.Tensor, gam: torch.Tensor, add: torch.Tensor | None = None):
+def recur_bwd_sum(
+    gr: torch.Tensor, gb: torch.Tensor, dz: torch.Tensor, gam: torch.Tensor, add: torch.Tensor | None = None,
+    gg_dtype: torch.dtype = torch.float32,
+):
     c = gr.shape[-1]
     rows = gr.numel() // c
     gsum, gdz = torch.empty_like(gr), torch.empty_like(gr)
-    gg = torch.empty((c,), device=gr.device, dtype=torch.float32)
+    gg = torch.empty((c,), device=gr.device, dtype=gg_dtype)
     ws = torch.empty((max(_abi.recur_bwd_workspace_bytes(rows, c), 16),), device=gr.device, dtype=torch.uint8)
     rc = _lib().lthc_recur_bwd_sum(
         gr.data_ptr(), gb.data_ptr(), dz.data_ptr(), _abi.ptr(add), _abi.code(gr), gam.data_ptr(), _abi.code(gam),
-        gsum.data_ptr(), gdz.data_ptr(), gg.data_ptr(), rows, c, ws.data_ptr(), ws.numel(), _stream(),
+        gsum.data_ptr(), gdz.data_ptr(), gg.data_ptr(), _abi.code(gg), rows, c, ws.data_ptr(), ws.numel(), _stream(),
     )  # fmt: skip
     _abi.check(rc, "lthc_recur_bwd_sum")
     return gsum, gdz, gg

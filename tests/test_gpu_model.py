@@ -132,6 +132,13 @@ def test_lazy_gamma_rounded_matches_block_hooks(dtype):
     gb = torch.autograd.grad([ops.lazy_gamma_rounded_eager(m.shared_read.alpha(), betas, dtype)], leaves, [g])
     for a, b in zip(ga, gb):
         assert ((a - b).abs().max() / b.abs().max().clamp_min(1e-30)).item() <= 1e-5
+    # the native backward (lthc_gamma_rounded_bwd) gives eager autograd's values bit for bit
+    al = m.shared_read.alpha().detach().requires_grad_(True)
+    bl = [b.detach().clone().requires_grad_(True) for b in betas]
+    na = torch.autograd.grad([ops.lazy_gamma_rounded(al, bl, dtype)], [al] + bl, [g])
+    ea = torch.autograd.grad([ops.lazy_gamma_rounded_eager(al, bl, dtype)], [al] + bl, [g])
+    for i, (a, b) in enumerate(zip(na, ea)):
+        assert a.dtype == b.dtype and torch.equal(a, b), f"gradient {i}: {(a != b).float().mean().item():.2e} differ"
 
 
 def test_forward_lazy_one_launch_gammas_equal_block_hooks(monkeypatch):

@@ -271,6 +271,10 @@ def test_recurrence_backward_with_branch_gradient(coracle, xdt, with_add, rows_c
     else:
         assert np.abs(host(gdz) - rgdz).max() <= 2e-2 * max(1.0, np.abs(rgdz).max())
     assert_f32(host(gg), rgg, tol=1e-5, what="ggamma")
+    if xdt != F32:  # ggamma written in a 16-bit gamma dtype: the fp32 sum rounded once, as a cast of it
+        _, _, gg16 = capi.recur_bwd_sum(g, gb, dz, gam.to(xdt), add, gg_dtype=xdt)
+        _, _, gg32 = capi.recur_bwd_sum(g, gb, dz, gam.to(xdt), add)
+        assert torch.equal(gg16, gg32.to(xdt))
 
 
 def test_split_steps_gradients_equal_unsplit_bf16():
