@@ -31,6 +31,8 @@ EXPORTS = (
     "lthc_materialise_fwd",
     "lthc_weight_grad_workspace_bytes",
     "lthc_weight_grad",
+    "lthc_materialise_bwd_workspace_bytes",
+    "lthc_materialise_bwd",
     "lthc_gamma",
     "lthc_gamma_rounded",
     "lthc_gamma_rounded_bwd",
@@ -82,6 +84,7 @@ def load() -> ctypes.CDLL:
         "lthc_read_multi_fwd": [vp, ci, pp, ci, pp, i64, i64, i64, i64, ci, vp],
         "lthc_materialise_fwd": [vp, pp, ci, pp, ci, vp, i64, i64, i64, i64, ci, vp],
         "lthc_weight_grad": [vp, pp, ci, vp, i64, i64, i64, i64, ci, vp, sz, vp],
+        "lthc_materialise_bwd": [vp, ci, pp, pp, ci, pp, vp, i64, i64, i64, i64, ci, vp, sz, vp],
         "lthc_gamma": [vp, pp, ci, vp, ci, i64, i64, ci, vp],
         "lthc_gamma_rounded": [vp, ci, pp, ci, vp, ci, i64, i64, ci, vp],
         "lthc_gamma_rounded_bwd": [vp, vp, ci, pp, ci, vp, pp, ci, i64, i64, ci, vp],
@@ -112,6 +115,8 @@ def load() -> ctypes.CDLL:
         fn.restype = ci
     lib.lthc_weight_grad_workspace_bytes.argtypes = [i64, i64, i64, i64, ci]
     lib.lthc_weight_grad_workspace_bytes.restype = sz
+    lib.lthc_materialise_bwd_workspace_bytes.argtypes = [i64, i64, i64, i64, ci]
+    lib.lthc_materialise_bwd_workspace_bytes.restype = sz
     lib.lthc_recur_bwd_workspace_bytes.argtypes = [i64, i64]
     lib.lthc_recur_bwd_workspace_bytes.restype = sz
     lib.lthc_ws_accumulate_bwd_workspace_bytes.argtypes = [i64, i64, ci]
@@ -158,6 +163,10 @@ def stream_of(t: torch.Tensor) -> int:
 
 def weight_grad_workspace_bytes(B: int, G: int, S: int, C: int, L: int) -> int:
     return int(load().lthc_weight_grad_workspace_bytes(B, G, S, C, L))
+
+
+def materialise_bwd_workspace_bytes(B: int, G: int, S: int, C: int, L: int) -> int:
+    return int(load().lthc_materialise_bwd_workspace_bytes(B, G, S, C, L))
 
 
 def recur_bwd_workspace_bytes(rows: int, C: int) -> int:

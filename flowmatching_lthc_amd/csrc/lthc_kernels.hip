@@ -1969,3 +1969,5 @@ int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, cons
 #include "decoder.inc"
 // One-launch dtype conversion of many weights (autocast's per-forward casts).
 #include "cast_many.inc"
+// Fused materialise backward (gdZ and gbeta from one pass over G).
+#include "materialise_bwd.inc"

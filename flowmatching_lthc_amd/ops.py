@@ -163,6 +163,51 @@ def _launch_weight_grad(high: Tensor, lows: Sequence[Tensor]) -> Tensor:
     return out
 
 
+def _launch_materialise_bwd(gr: Tensor, dzs: Sequence[Tensor], betas: Sequence[Tensor], outs: Sequence[Tensor]) -> Tensor:
+    """gdZ_l into outs and the fp32 [L,C,16] gbeta from one pass over gr (lthc_materialise_bwd)."""
+    b, g, c = _hi_geom(gr, "grad_out")
+    L = len(dzs)
+    gb = torch.empty((L, c, K), device=gr.device, dtype=torch.float32)
+    nbytes = _abi.materialise_bwd_workspace_bytes(b, g, S, c, L)
+    ws = torch.empty((max(nbytes, 16),), device=gr.device, dtype=torch.uint8)
+    with _on_device(gr):
+        rc = _abi.load().lthc_materialise_bwd(
+            gr.data_ptr(), _abi.code(gr), _abi.ptr_array(dzs), _abi.ptr_array(betas), _abi.code(betas[0]),
+            _abi.ptr_array(outs), gb.data_ptr(), b, g, S, c, L, ws.data_ptr(), ws.numel(), _abi.stream_of(gr),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_materialise_bwd")
+    return gb
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_backward", mutates_args=())
+def final_accumulate_backward(grad_out: Tensor, dzs: list[Tensor], betas: list[Tensor]) -> tuple[Tensor, Tensor]:
+    """(gdZ stack [L,B,M,C] in grad_out.dtype, fp32 [L,C,16] gbeta) of X_L = x0 + sum_l P_l(dz_l): the results of
+    the two reference backward ops (_grad_dz_ptr, _grad_beta_ptr) from one pass over grad_out."""
+    _on_gpu(grad_out, *dzs, *betas)
+    b, g, c = _hi_geom(grad_out, "grad_out")
+    L = len(dzs)
+    if L != len(betas) or not 1 <= L <= _abi.MAX_LAYERS:
+        raise ValueError(f"expected 1..{_abi.MAX_LAYERS} dz and as many beta tensors, got {len(dzs)} and {len(betas)}")
+    for i, (dz, bt) in enumerate(zip(dzs, betas)):
+        if tuple(dz.shape) != (b, g * g, c):
+            raise ValueError(f"dz[{i}] must be [{b},{g * g},{c}], got {tuple(dz.shape)}")
+        _check_weight(bt, c, f"beta[{i}]")
+    grad_out = _prep(grad_out)
+    dzs = _same_dtype(grad_out, [_prep(d) for d in dzs])
+    betas = [_prep_w(bt, grad_out.dtype) for bt in betas]
+    if len({bt.dtype for bt in betas}) != 1:
+        betas = [_prep_w(bt.float(), grad_out.dtype) for bt in betas]
+    gdz = torch.empty((L, b, g * g, c), device=grad_out.device, dtype=grad_out.dtype)
+    gb = _launch_materialise_bwd(grad_out, dzs, betas, list(gdz.unbind(0)))
+    return gdz, gb
+
+
+@final_accumulate_backward.register_fake
+def _(grad_out: Tensor, dzs: list[Tensor], betas: list[Tensor]):
+    b, g, c = _hi_geom(grad_out, "grad_out")
+    return grad_out.new_empty((len(dzs), b, g * g, c)), grad_out.new_empty((len(dzs), c, K), dtype=torch.float32)
+
+
 # ---------------------------------------------------------------------------
 # READ  (jit_thc::local_write_traceable, local_thc_triton_kernels.py:2673-2683)
 # ---------------------------------------------------------------------------
@@ -479,6 +524,9 @@ def _backward_final_accumulate(ctx, grad_out):
     # local_thc_triton_kernels.py:1652-1660: grad_x0 is grad_out itself.
     dz_stack, beta_stack = ctx.saved_tensors
     grad_out = grad_out.contiguous()
+    if ctx.needs_input_grad[1] and ctx.needs_input_grad[2]:  # both from one pass over grad_out
+        grad_dz, gb = final_accumulate_backward(grad_out, list(dz_stack.unbind(0)), list(beta_stack.unbind(0)))
+        return grad_out, grad_dz, gb.to(dtype=beta_stack.dtype)
     grad_dz = final_accumulate_b4_grad_dz_traceable(grad_out, beta_stack) if ctx.needs_input_grad[1] else None
     grad_beta = None
     if ctx.needs_input_grad[2]:
@@ -578,6 +626,9 @@ def _backward_final_accumulate_list(ctx, grad_out):
     saved = ctx.saved_tensors
     dzs, betas = saved[: ctx.L], saved[ctx.L :]
     grad_out = grad_out.contiguous()
+    if ctx.needs_input_grad[1] and ctx.needs_input_grad[2]:  # both from one pass over grad_out
+        gdz, gb = final_accumulate_backward(grad_out, list(dzs), list(betas))
+        return grad_out, list(gdz.unbind(0)), [g.to(dtype=bt.dtype) for g, bt in zip(gb.unbind(0), betas, strict=True)]
     grad_dzs = final_accumulate_list_grad_dz(grad_out, list(betas)) if ctx.needs_input_grad[1] else None
     grad_betas = None
     if ctx.needs_input_grad[2]:
@@ -694,6 +745,10 @@ def _backward_final_accumulate_12(ctx, grad_out):
     need = ctx.needs_input_grad
     grad_dzs = (None,) * 12
     grad_betas = (None,) * 12
+    if any(need[1:13]) and any(need[13:25]):  # both from one pass over grad_out
+        gdz, gb = final_accumulate_backward(grad_out, list(dzs), list(betas))
+        grad_betas = tuple(g.to(dtype=bt.dtype) for g, bt in zip(gb.unbind(0), betas, strict=True))
+        return (grad_out, *gdz.unbind(0), *grad_betas)
     if any(need[1:13]):
         grad_dzs = tuple(final_accumulate_b4_12_grad_dz_ptr_traceable(grad_out, *betas).unbind(0))
     if any(need[13:25]):

@@ -129,6 +129,23 @@ int lthc_weight_grad(const void* high, const void* const* low, int x_dtype, floa
                      void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * MATERIALISE BACKWARD (gdZ and gbeta in one pass over G)
+ *   gdz_l[cell, c]  = sum_k beta_l[c,k] G[cell,k,c]      (x_dtype, fp32 accumulation, k in order)
+ *   gbeta[l, c, k]  = sum_cells G[cell,k,c] dz_l[cell,c] (fp32 [L, C, 16], fixed-order reduction)
+ * Replaces final_accumulate_b4_12_grad_dz_ptr + final_accumulate_b4_12_grad_beta_ptr
+ * (local_thc_triton_kernels.py:512-680, 1800-1894): the same two results as
+ * lthc_read_multi_fwd(G, beta) and lthc_weight_grad(G, dz), but G (the
+ * largest tensor) is read once instead of twice.  gdz is bitwise equal to
+ * lthc_read_multi_fwd's.  One kernel when L <= 24, C % 64 == 0 and G is
+ * below 4 GiB; otherwise the two separate passes.  `dz`, `beta`, `gdz`
+ * are host arrays of L device pointers; the workspace holds the fp32 partials.
+ */
+size_t lthc_materialise_bwd_workspace_bytes(int64_t B, int64_t G, int64_t s, int64_t C, int L);
+int lthc_materialise_bwd(const void* g, int x_dtype, const void* const* dz, const void* const* beta, int w_dtype,
+                         void* const* gdz, float* gbeta, int64_t B, int64_t G, int64_t s, int64_t C, int L,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * GAMMA   gamma_l[c] = sum_k alpha[c,k] * beta_l[c,k]   (written in out_dtype)
  * Replaces LayerLocalWrite.gamma_from_alpha (local_thc.py:1278-1283), computed
  * here in fp32 from the given weights.  `beta` is a host array of L device

@@ -64,6 +64,22 @@ def weight_grad(high: torch.Tensor, lows) -> torch.Tensor:
     return out
 
 
+def materialise_bwd(gr: torch.Tensor, dzs, betas) -> tuple[list[torch.Tensor], torch.Tensor]:
+    b, h, _, c = gr.shape
+    g = h // S
+    L = len(dzs)
+    outs = [torch.empty((b, g * g, c), device=gr.device, dtype=gr.dtype) for _ in dzs]
+    gb = torch.empty((L, c, S * S), device=gr.device, dtype=torch.float32)
+    nbytes = _abi.materialise_bwd_workspace_bytes(b, g, S, c, L)
+    ws = torch.empty((max(nbytes, 16),), device=gr.device, dtype=torch.uint8)
+    rc = _lib().lthc_materialise_bwd(
+        gr.data_ptr(), _abi.code(gr), _abi.ptr_array(dzs), _abi.ptr_array(betas), _abi.code(betas[0]),
+        _abi.ptr_array(outs), gb.data_ptr(), b, g, S, c, L, ws.data_ptr(), ws.numel(), _stream(),
+    )  # fmt: skip
+    _abi.check(rc, "lthc_materialise_bwd")
+    return outs, gb
+
+
 def gamma(alpha: torch.Tensor, betas, out_dtype=torch.float32) -> torch.Tensor:
     c, k = alpha.shape
     out = torch.empty((len(betas), c), device=alpha.device, dtype=out_dtype)

@@ -327,6 +327,68 @@ def test_config5_shape_bf16(coracle):
     assert_f32(host(capi.weight_grad(g, dzs)), coracle.Cweight_grad(gh, dzh, G), what="gbeta")
 
 
+@pytest.mark.parametrize(
+    "B,G,C,L,xdt,wdt",
+    [
+        (4, 16, 768, 12, BF16, F32),   # configuration 3's layer count and width, the fused pass
+        (2, 16, 768, 5, BF16, F32),    # padded depth bucket (8)
+        (2, 16, 128, 1, torch.float16, torch.float16),
+        (2, 8, 64, 4, F32, F32),
+        (1, 32, 1024, 12, BF16, BF16),  # configuration 5's grid and width
+        (2, 16, 768, 13, BF16, F32),   # padded depth-24 bucket (four layer groups)
+        (1, 32, 1024, 24, BF16, F32),  # configuration 5's grid, width and depth
+        (1, 8, 64, 25, BF16, F32),     # deeper than the fused kernel: the two separate passes
+        (2, 4, 260, 3, BF16, F32),     # C not a multiple of 64: the two separate passes
+    ],
+)
+def test_materialise_backward_fused_pass(coracle, B, G, C, L, xdt, wdt):
+    """lthc_materialise_bwd: gdZ bitwise equal to lthc_read_multi_fwd, gbeta equal to lthc_weight_grad up to the
+    summation order (same cells, partials grouped differently), both against the oracle."""
+    print(f"case B={B} G={G} C={C} L={L} x={xdt} w={wdt}", flush=True)
+    d = cfg(B, G, C, L, seed=L + C, grads=True)
+    g = dev(d["grad_xl"], xdt)
+    betas = [dev(b, wdt) for b in d["beta"]]
+    dzs = [dev(z, xdt) for z in d["dz"]]
+    gdz, gb = capi.materialise_bwd(g, dzs, betas)
+    for l, (a, r) in enumerate(zip(gdz, capi.read_multi(g, betas))):
+        assert torch.equal(a, r), f"gdZ_{l} differs from lthc_read_multi_fwd"
+    sep = capi.weight_grad(g, dzs)
+    assert_f32(host(gb), host(sep), tol=1e-5, what="gbeta vs lthc_weight_grad")
+    gh, dzh = host(g), [host(z) for z in dzs]
+    bh = [host(b) for b in betas]
+    ref_dz = coracle.Cread_multi(gh, bh, G)
+    for l in range(L):
+        if xdt == F32:
+            assert_f32(host(gdz[l]), ref_dz[l], what=f"gdZ_{l}")
+        else:
+            assert np.abs(host(gdz[l]) - ref_dz[l]).max() <= 2e-2 * max(1.0, np.abs(ref_dz[l]).max())
+    assert_f32(host(gb), coracle.Cweight_grad(gh, dzh, G), tol=1e-5, what="gbeta")
+    again = capi.materialise_bwd(g, dzs, betas)
+    assert torch.equal(again[1], gb), "gbeta is not reproducible run to run"
+
+
+def test_final_accumulate_backward_op_matches_reference_ops():
+    """jit_thc::final_accumulate_backward equals the reference's two backward ops (gdZ bitwise, gbeta to 1e-5), and
+    the 12-pointer op's autograd, which uses it, gives the same gradients."""
+    B, G, C, L = 2, 16, 768, 12
+    d = cfg(B, G, C, L, seed=21, grads=True)
+    g = dev(d["grad_xl"], BF16)
+    betas = [dev(b) for b in d["beta"]]
+    dzs = [dev(z, BF16) for z in d["dz"]]
+    gdz, gb = ops.final_accumulate_backward(g, dzs, betas)
+    assert torch.equal(gdz, ops.final_accumulate_b4_12_grad_dz_ptr_traceable(g, *betas))
+    ref_gb = ops.final_accumulate_b4_12_grad_beta_ptr_traceable(g, *dzs)
+    assert_f32(host(gb), host(ref_gb), tol=1e-5, what="gbeta")
+    x0 = dev(d["x0"], BF16).requires_grad_(True)
+    bl = [b.clone().requires_grad_(True) for b in betas]
+    zl = [z.clone().requires_grad_(True) for z in dzs]
+    ops.final_accumulate_b4_12_traceable(x0, *zl, *bl).backward(g)
+    assert torch.equal(x0.grad, g)
+    for l in range(L):
+        assert torch.equal(zl[l].grad, gdz[l])
+        assert torch.equal(bl[l].grad, gb[l])
+
+
 def test_config5_list_op_and_autograd_bf16(coracle):
     """jit_thc::final_accumulate_list at configuration 5's shape: forward, and its autograd (gdZ_l, gbeta_l)."""
     B, G, C, L = 2, 32, 1024, 24
