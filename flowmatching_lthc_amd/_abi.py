@@ -53,6 +53,7 @@ EXPORTS = (
     "lthc_swiglu",
     "lthc_gate_add_norm_modulate_fwd",
     "lthc_gate_residual",
+    "lthc_block_tail_fwd",
 )
 
 _lib = None
@@ -107,6 +108,9 @@ def load() -> ctypes.CDLL:
             vp, vp, vp, ci, vp, ci, vp, vp, i64, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp,
         ],  # fmt: skip
         "lthc_gate_residual": [vp, vp, i64, vp, ci, vp, i64, i64, i64, vp],
+        "lthc_block_tail_fwd": [
+            vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, vp, i64, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp,
+        ],  # fmt: skip
         "lthc_norm_modulate_bwd": [vp, vp, ci, vp, ci, vp, i64, vp, vp, vp, vp, vp, i64, i64, i64, vp, sz, vp],
     }
     for name, args in sig.items():

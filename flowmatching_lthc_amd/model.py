@@ -326,13 +326,30 @@ class WorkspaceSharedAdaLNBranch(nn.Module):
     def forward(self, z: torch.Tensor, t6: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> torch.Tensor:
         sh_a, sc_a, g_a, sh_m, sc_m, g_m = t6.chunk(6, dim=-1)
         a = self.attn(norm_modulate(self.norm1, z, sh_a, sc_a), rope)
-        if z.is_cuda and z.dim() == 3 and a.dtype == z.dtype == t6.dtype and z.shape[-1] % 8 == 0 and z.shape[-1] <= 2048:
+        if self.fused_gates(z, a, t6):
             # d_attn = g_a * a, z + d_attn and its pre-norm in one HIP pass; d_attn + g_m * mlp in another
             d_attn, h = ops_branch.gate_add_norm_modulate(z, a, g_a, self.norm2.weight, sh_m, sc_m, self.norm2.eps)
             return ops_branch.gate_residual(d_attn, g_m, self.mlp(h))
         d_attn = g_a.unsqueeze(1) * a
         d_mlp = g_m.unsqueeze(1) * self.mlp(norm_modulate(self.norm2, z + d_attn, sh_m, sc_m))
         return d_attn + d_mlp
+
+    @staticmethod
+    def fused_gates(z: torch.Tensor, a: torch.Tensor, t6: torch.Tensor) -> bool:
+        """The gated residuals run as HIP passes: GPU, [B, N, C] with C % 8 == 0 and C <= 2048, one dtype."""
+        return z.is_cuda and z.dim() == 3 and a.dtype == z.dtype == t6.dtype and z.shape[-1] % 8 == 0 and z.shape[-1] <= 2048
+
+    def parts(
+        self, z: torch.Tensor, t6: torch.Tensor, rope: VisionRotaryEmbeddingFast, y1: torch.Tensor | None = None
+    ) -> tuple[torch.Tensor, torch.Tensor] | None:
+        """(g_a * attn, mlp output): forward() without its last gated residual, or None where the gated residuals
+        are not HIP passes.  y1: this branch's first pre-norm output when the caller has computed it."""
+        sh_a, sc_a, g_a, sh_m, sc_m, _ = t6.chunk(6, dim=-1)
+        a = self.attn(y1 if y1 is not None else norm_modulate(self.norm1, z, sh_a, sc_a), rope)
+        if not self.fused_gates(z, a, t6):
+            return None
+        d_attn, h = ops_branch.gate_add_norm_modulate(z, a, g_a, self.norm2.weight, sh_m, sc_m, self.norm2.eps)
+        return d_attn, self.mlp(h)
 
 
 class FinalLayerSharedAdaLN(nn.Module):
@@ -494,6 +511,9 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
         self.fused_decoder = True
         # inference under autocast with fp32 parameters: all weight conversions in one launch
         self.batched_weight_cast = True
+        # inference: each block's last gated residual, its recurrence step and the next block's first pre-norm in
+        # one HIP pass (jit_thc::block_tail)
+        self.fused_block_tail = True
 
     # -- initialisation (local_thc.py:944-970, :1004-1007) ------------------------------------------
     def initialize_weights(self) -> None:
@@ -567,6 +587,10 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
         # and the recurrence steps are the fused-backward forms: same values, x0's, each dZ_l's and each Z_l's
         # gradient from one kernel instead of a kernel plus autograd's add.
         x0, z = self.shared_read.read_with_residual(self.x_embedder(x))
+        if self._tail_fusable(z):
+            dz_list = self._blocks_fused_tail(z, t6)
+            if dz_list is not None:
+                return self._decode(self.final_accumulate_reference(x0, dz_list), t2)
         zb = z  # the next branch's input: z itself, or the step's branch output (same values)
         dz_list, gammas = [], None
         for i, block in enumerate(self.blocks):
@@ -580,6 +604,52 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
                 z, zb, dz = block.lazy_workspace_step(z, dz, self.shared_read, gammas[i], split=True)
             dz_list.append(dz)
         return self._decode(self.final_accumulate_reference(x0, dz_list), t2)
+
+    def _tail_fusable(self, z: torch.Tensor) -> bool:
+        """Inference on the GPU with the standard blocks, hooks, branch and ungrouped weights: jit_thc::block_tail
+        applies."""
+        std = SharedReadLocalTHCSharedAdaLNJiTBlock
+        return (
+            self.fused_block_tail
+            and not torch.is_grad_enabled()
+            and z.is_cuda
+            and len(self.blocks) > 1
+            and self.shared_read.group_dim == 1
+            and all(
+                blk.write.group_dim == 1
+                and type(blk) is std
+                and not {"branch_update", "lazy_workspace_step", "lazy_workspace_update"} & blk.__dict__.keys()
+                and type(blk.branch) is WorkspaceSharedAdaLNBranch
+                and "forward" not in blk.branch.__dict__
+                for blk in self.blocks
+            )
+        )
+
+    def _blocks_fused_tail(self, z: torch.Tensor, t6: torch.Tensor) -> list[torch.Tensor] | None:
+        """The block loop of forward_lazy with each block's gate_residual, its recurrence step and the next block's
+        first pre-norm as one jit_thc::block_tail pass: the same values as the hook path.  Returns the dZ list, or
+        None (nothing computed that the caller keeps) when the first block's gated residuals are not HIP passes."""
+        sh_a, sc_a, _, _, _, g_m = t6.chunk(6, dim=-1)
+        dz_list, gammas, y1 = [], None, None
+        nb = len(self.blocks)
+        for i, block in enumerate(self.blocks):
+            parts = block.branch.parts(z, t6, self.workspace_rope, y1)
+            if parts is None:
+                if i == 0:
+                    return None
+                raise RuntimeError("the blocks' gated residuals changed path between blocks")
+            d_attn, mo = parts
+            if i == 0:
+                gammas = self._all_gammas(d_attn)
+                if gammas is None:
+                    return None
+            if i + 1 < nb:
+                n1 = self.blocks[i + 1].branch.norm1
+                dz, z, y1 = ops_branch.block_tail(z, d_attn, g_m, mo, gammas[i], n1.weight, sh_a, sc_a, n1.eps)
+            else:  # the last step's Z_L feeds nothing
+                dz = ops_branch.gate_residual(d_attn, g_m, mo)
+            dz_list.append(dz)
+        return dz_list
 
     def _all_gammas(self, dz: torch.Tensor) -> list[torch.Tensor] | None:
         """Every block's gamma_from_alpha(shared_read.alpha(dz.dtype)) in one launch (ops.lazy_gamma_rounded: the

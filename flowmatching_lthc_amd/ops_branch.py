@@ -18,7 +18,11 @@ activation dtype), registered as a ``jit_thc`` custom op:
 * ``jit_thc::gate_add_norm_modulate``: ``dz_attn = gate_msa * attn``,
   ``z_tmp = z + dz_attn`` and ``modulate(norm2(z_tmp), ...)`` of
   ``WorkspaceSharedAdaLNBranch.forward`` (local_thc.py:319-322);
-* ``jit_thc::gate_residual``: its ``dz_attn + gate_mlp * mlp`` (:322-323).
+* ``jit_thc::gate_residual``: its ``dz_attn + gate_mlp * mlp`` (:322-323);
+* ``jit_thc::block_tail`` (inference): that gate_residual, the lazy
+  recurrence step ``Z_{l+1} = Z_l + gamma_l * dZ_l`` (local_thc.py:1325-1328)
+  and the next block's first pre-norm (:315-317) in one pass, each value
+  that of the three separate ops.
 
 The backward of all but gate_residual recomputes the eager sequence under
 autograd (the forward's values are those of that sequence; the attention's
@@ -378,3 +382,46 @@ def _backward_gres(ctx, grad):
 
 
 torch.library.register_autograd(gate_residual, _backward_gres, setup_context=_setup_gres_ctx)
+
+
+# ---------------------------------------------------------------------------
+# block tail (inference): gate_residual + recurrence step + the next block's first pre-norm
+# ---------------------------------------------------------------------------
+@torch.library.custom_op("jit_thc::block_tail", mutates_args=())
+def block_tail(
+    z: Tensor, a: Tensor, gate: Tensor, m: Tensor, gamma: Tensor, weight: Tensor, shift: Tensor, scale: Tensor,
+    eps: float,
+) -> tuple[Tensor, Tensor, Tensor]:
+    """(dz, z_next, y) = (a + gate * m, z + gamma * dz, modulate(RMSNorm(z_next), shift, scale)) in z's dtype, one
+    pass: gate_residual, lazy_workspace_update and the next block's norm_modulate with the same values.  z, a, m
+    [B,N,C]; gate, shift, scale [B,C]; gamma and weight [C].  Forward only (inference)."""
+    _on_gpu(z, a, gate, m, gamma, weight, shift, scale)
+    if z.dim() != 3 or z.shape[2] % 8 != 0:
+        raise ValueError(f"z must be [B,N,C] with C % 8 == 0, got {tuple(z.shape)}")
+    b, n, c = z.shape
+    _check_bnc("a", a, (b, n, c), z.dtype)
+    _check_bnc("m", m, (b, n, c), z.dtype)
+    for name, t in (("gate", gate), ("shift", shift), ("scale", scale)):
+        _check_bnc(name, t, (b, c), z.dtype)
+    for name, t in (("gamma", gamma), ("weight", weight)):
+        if tuple(t.shape) != (c,):
+            raise ValueError(f"{name} must be [{c}], got {tuple(t.shape)}")
+    _abi.code(z)
+    z, a, m = _aligned(z), _aligned(a), _aligned(m)
+    (gate, shift, scale), ld = _mod_rows(gate, shift, scale)
+    w = _norm_weight(weight)
+    g = _norm_weight(gamma)
+    dz, zn, y = torch.empty_like(z), torch.empty_like(z), torch.empty_like(z)
+    with _on_device(z):
+        rc = _abi.load().lthc_block_tail_fwd(
+            z.data_ptr(), a.data_ptr(), m.data_ptr(), gate.data_ptr(), _abi.code(z), g.data_ptr(), _abi.code(g),
+            w.data_ptr(), _abi.code(w), shift.data_ptr(), scale.data_ptr(), ld, dz.data_ptr(), zn.data_ptr(),
+            y.data_ptr(), b, n, c, eps, _abi.stream_of(z),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_block_tail_fwd")
+    return dz, zn, y
+
+
+@block_tail.register_fake
+def _(z, a, gate, m, gamma, weight, shift, scale, eps):
+    return torch.empty_like(z), torch.empty_like(z), torch.empty_like(z)

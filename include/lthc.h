@@ -369,6 +369,23 @@ int lthc_gate_add_norm_modulate_fwd(const void* z, const void* a, const void* ga
 int lthc_gate_residual(const void* d, const void* gate, int64_t gate_ld, const void* m, int x_dtype, void* out,
                        int64_t B, int64_t N, int64_t C, void* stream);
 
+/*
+ * BLOCK TAIL (inference): one block's last gated residual, the lazy
+ * recurrence step and the next block's first pre-norm in one pass.  Per token
+ * t of sample b, channel c (z = Z_l, a = the attention's gated residual
+ * g_a * attn, m = the MLP output, gate = g_m):
+ *   dz[t,c]     = r(a[t,c] + r(gate[b,c] * m[t,c]))     (lthc_gate_residual)
+ *   z_next[t,c] = r(fma(gamma[c], dz[t,c], z[t,c]))       (lthc_recur_fwd)
+ *   y[t,:]      = lthc_norm_modulate_fwd of z_next with weight, shift, scale
+ * (local_thc.py:319-323 of block l, :1325-1328, :315-317 of block l + 1),
+ * each value bitwise that of the three entry points in sequence.  gate,
+ * shift and scale are rows of stride mod_ld; gamma is [C] in g_dtype.
+ */
+int lthc_block_tail_fwd(const void* z, const void* a, const void* m, const void* gate, int x_dtype, const void* gamma,
+                        int g_dtype, const void* weight, int w_dtype, const void* shift, const void* scale,
+                        int64_t mod_ld, void* dz, void* z_next, void* y, int64_t B, int64_t N, int64_t C, float eps,
+                        void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -405,3 +405,77 @@ def test_model_fused_decoder_matches_unfused_bf16():
 
     assert rel(outs[True], outs[False]) <= 2e-2, rel(outs[True], outs[False])
     assert rel(outs[True]) <= max(1.5 * rel(outs[False]), 1e-3), (rel(outs[True]), rel(outs[False]))
+
+
+# ---------------------------------------------------------------------------
+# jit_thc::block_tail (inference: gate_residual + recurrence step + next pre-norm)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,gdt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
+                                       (torch.float16, torch.float16), (torch.float32, torch.float32)])
+@pytest.mark.parametrize("C", [768, 1024, 136])
+def test_block_tail_equals_the_three_ops(dtype, gdt, C):
+    """block_tail gives dz, Z_{l+1} and the next pre-norm bit for bit as gate_residual, lazy_workspace_update and
+    norm_modulate do in sequence (the AdaLN rows as strided chunks of one [B, 6C] buffer, as in the model)."""
+    from flowmatching_lthc_amd import ops
+
+    print(f"case dtype={dtype} gamma={gdt} C={C}", flush=True)
+    B, N = 3, 256
+    gen = torch.Generator().manual_seed(C)
+    z, a, m = ((torch.randn((B, N, C), generator=gen) * s).to(DEV, dtype) for s in (1.0, 0.1, 0.5))
+    t6 = (torch.randn((B, 6 * C), generator=gen) * 0.3).to(DEV, dtype)
+    sh_a, sc_a, _, _, _, g_m = t6.chunk(6, dim=-1)
+    gamma = (torch.randn(C, generator=gen) * 0.05).to(DEV, gdt)
+    w = (torch.randn(C, generator=gen) * 0.1 + 1).to(DEV)
+    with torch.no_grad():
+        dz, zn, y = OB.block_tail(z, a, g_m, m, gamma, w, sh_a, sc_a, 1e-6)
+        rdz = OB.gate_residual(a, g_m, m)
+        rzn = ops.lazy_workspace_update(z, rdz, gamma)
+        ry = ops.norm_modulate(rzn, w, sh_a, sc_a, 1e-6)[0]
+    assert torch.equal(dz, rdz), "dz"
+    assert torch.equal(zn, rzn), "z_next"
+    assert torch.equal(y, ry), "next pre-norm"
+
+
+def test_model_fused_block_tail_equals_hook_path():
+    """LTHC-B/4 forward under no-grad bf16 autocast: the fused block tails give the hook path's output bit for bit,
+    also captured in a HIP graph and replayed; with gradients enabled the model keeps the hook path."""
+    m = M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=12).to(DEV).eval()
+    gen = torch.Generator().manual_seed(14)
+    x = torch.randn((2, 3, 256, 256), generator=gen).to(DEV)
+    t = torch.rand((2,), generator=gen).to(DEV)
+    y = torch.tensor([7, 512], device=DEV)
+    calls = []
+    orig = OB.block_tail
+
+    def spy(*args):
+        calls.append(1)
+        return orig(*args)
+
+    OB.block_tail = spy
+    try:
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            m.fused_block_tail = True
+            a = m(x, t, y)
+            assert len(calls) == len(m.blocks) - 1, "the fused tail path did not run"
+            m.fused_block_tail = False
+            b = m(x, t, y)
+            m.fused_block_tail = True
+            s = torch.cuda.Stream()
+            s.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(s):
+                m(x, t, y)
+            torch.cuda.current_stream().wait_stream(s)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                c = m(x, t, y)
+        for _ in range(3):
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(c, a)
+        assert torch.equal(a, b)
+        calls.clear()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            m(x, t, y).float().sum().backward()
+        assert not calls, "the training forward must keep the hook path"
+    finally:
+        OB.block_tail = orig
