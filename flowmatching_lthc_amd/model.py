@@ -152,7 +152,15 @@ class BottleneckPatchEmbedNHWC(nn.Module):
         b, cin = x.shape[:2]
         p = self.patch_size[0]
         gh, gw = self.grid_size
-        patches = x.reshape(b, cin, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5).reshape(b, gh, gw, cin * p * p)
+        view = x.reshape(b, cin, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5)
+        if x.is_cuda and x.dtype == torch.float32 and torch.is_autocast_enabled("cuda"):
+            # autocast would cast the gathered fp32 patches to its dtype for proj1: gather and cast in one copy
+            # (the same round-to-nearest-even values)
+            dt = torch.get_autocast_dtype("cuda")
+            patches = torch.empty((b, gh, gw, cin, p, p), device=x.device, dtype=dt).copy_(view)
+            patches = patches.view(b, gh, gw, cin * p * p)
+        else:
+            patches = view.reshape(b, gh, gw, cin * p * p)
         cast = self.__dict__.get("_cast")
         w1, w2, b2 = cast if cast is not None else (self.proj1.weight, self.proj2.weight, self.proj2.bias)
         h = F.linear(patches, w1.view(self.proj1.out_channels, -1))

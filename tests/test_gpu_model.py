@@ -154,3 +154,22 @@ def test_forward_lazy_one_launch_gammas_equal_block_hooks(monkeypatch):
         b = m(x, t, y)
     d = (a.float() - b.float()).abs().max().item()
     assert d <= 1e-2 * b.float().abs().max().item(), d
+
+
+def test_patch_embed_gather_cast_equals_autocast_cast():
+    """Under bf16 autocast the patch embed gathers the fp32 patches straight into bf16; the embedding equals the one
+    from the fp32 gather that autocast then casts, bit for bit."""
+    import torch.nn.functional as F
+
+    m = M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=15).to(DEV).eval()
+    emb = m.x_embedder
+    x = torch.randn((2, 3, 256, 256), generator=torch.Generator().manual_seed(16)).to(DEV)
+    b, p = 2, emb.patch_size[0]
+    gh, gw = emb.grid_size
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+        got = emb(x)
+        patches = x.reshape(b, 3, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5).reshape(b, gh, gw, 3 * p * p)
+        h = F.linear(patches, emb.proj1.weight.view(emb.proj1.out_channels, -1))
+        ref = F.linear(h, emb.proj2.weight.view(emb.proj2.out_channels, -1), emb.proj2.bias)
+    assert got.dtype == ref.dtype == torch.bfloat16
+    assert torch.equal(got, ref)
