@@ -571,8 +571,9 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(
-            f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the interface shards along the "
-            "batch; see DESIGN.md for the multi-GPU plan)",
+            f"bench.py measures one GPU only: --gpus {args.gpus} is not supported (the interface would shard along "
+            "the batch: each GPU runs the same kernels on B/N samples and the weight gradients join the data-parallel "
+            "all-reduce)",
             file=sys.stderr,
         )
         sys.exit(2)
