@@ -164,10 +164,11 @@ def test_model_with_fused_branch_equals_eager_branch(monkeypatch):
             assert ((grads[n] - p.grad).abs().max() / scale).item() <= 1e-4, n
 
 
+@pytest.mark.parametrize("N", [256, 9])  # 256: the block-shared kernel; 9: the per-wavefront one
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_gated_residual_ops_match_eager(dtype):
-    print(f"case dtype={dtype}", flush=True)
-    B, N, C = 4, 256, 768
+def test_gated_residual_ops_match_eager(dtype, N):
+    print(f"case dtype={dtype} N={N}", flush=True)
+    B, C = 4, 768
     gen = torch.Generator().manual_seed(5)
     z, a, m = (torch.randn((B, N, C), generator=gen).to(DEV, dtype) for _ in range(3))
     gate, shift, scale = ((torch.randn((B, 6 * C), generator=gen) * 0.3).to(DEV, dtype)[:, :C] for _ in range(3))
@@ -412,14 +413,15 @@ def test_model_fused_decoder_matches_unfused_bf16():
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype,gdt", [(torch.bfloat16, torch.bfloat16), (torch.bfloat16, torch.float32),
                                        (torch.float16, torch.float16), (torch.float32, torch.float32)])
-@pytest.mark.parametrize("C", [768, 1024, 136])
-def test_block_tail_equals_the_three_ops(dtype, gdt, C):
+@pytest.mark.parametrize("C,N", [(768, 256), (1024, 256), (136, 256), (768, 7)])
+def test_block_tail_equals_the_three_ops(dtype, gdt, C, N):
     """block_tail gives dz, Z_{l+1} and the next pre-norm bit for bit as gate_residual, lazy_workspace_update and
-    norm_modulate do in sequence (the AdaLN rows as strided chunks of one [B, 6C] buffer, as in the model)."""
+    norm_modulate do in sequence (the AdaLN rows as strided chunks of one [B, 6C] buffer, as in the model).
+    N = 256 runs the block-shared kernel, N = 7 the per-wavefront one."""
     from flowmatching_lthc_amd import ops
 
-    print(f"case dtype={dtype} gamma={gdt} C={C}", flush=True)
-    B, N = 3, 256
+    print(f"case dtype={dtype} gamma={gdt} C={C} N={N}", flush=True)
+    B = 3
     gen = torch.Generator().manual_seed(C)
     z, a, m = ((torch.randn((B, N, C), generator=gen) * s).to(DEV, dtype) for s in (1.0, 0.1, 0.5))
     t6 = (torch.randn((B, 6 * C), generator=gen) * 0.3).to(DEV, dtype)
