@@ -54,6 +54,12 @@ EXPORTS = (
     "lthc_gate_add_norm_modulate_fwd",
     "lthc_gate_residual",
     "lthc_block_tail_fwd",
+    "lthc_recur_fwd_prefix",
+    "lthc_read_bwd_workspace_bytes",
+    "lthc_read_bwd",
+    "lthc_interface_workspace_bytes",
+    "lthc_interface_fwd",
+    "lthc_interface_bwd",
 )
 
 _lib = None
@@ -108,6 +114,12 @@ def load() -> ctypes.CDLL:
             vp, vp, vp, ci, vp, ci, vp, vp, i64, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp,
         ],  # fmt: skip
         "lthc_gate_residual": [vp, vp, i64, vp, ci, vp, i64, i64, i64, vp],
+        "lthc_recur_fwd_prefix": [vp, pp, ci, vp, ci, pp, i64, i64, ci, vp],
+        "lthc_read_bwd": [vp, vp, ci, vp, ci, vp, vp, vp, i64, i64, i64, i64, vp, sz, vp],
+        "lthc_interface_fwd": [vp, ci, vp, pp, ci, pp, pp, vp, i64, i64, i64, i64, ci, vp, sz, vp],
+        "lthc_interface_bwd": [
+            vp, pp, ci, vp, pp, vp, pp, ci, vp, pp, vp, vp, i64, i64, i64, i64, ci, vp, sz, vp,
+        ],  # fmt: skip
         "lthc_block_tail_fwd": [
             vp, vp, vp, vp, ci, vp, ci, vp, ci, vp, vp, i64, vp, vp, vp, i64, i64, i64, ctypes.c_float, vp,
         ],  # fmt: skip
@@ -121,6 +133,10 @@ def load() -> ctypes.CDLL:
     lib.lthc_weight_grad_workspace_bytes.restype = sz
     lib.lthc_materialise_bwd_workspace_bytes.argtypes = [i64, i64, i64, i64, ci]
     lib.lthc_materialise_bwd_workspace_bytes.restype = sz
+    lib.lthc_read_bwd_workspace_bytes.argtypes = [i64, i64, i64, i64]
+    lib.lthc_read_bwd_workspace_bytes.restype = sz
+    lib.lthc_interface_workspace_bytes.argtypes = [i64, i64, i64, i64, ci]
+    lib.lthc_interface_workspace_bytes.restype = sz
     lib.lthc_recur_bwd_workspace_bytes.argtypes = [i64, i64]
     lib.lthc_recur_bwd_workspace_bytes.restype = sz
     lib.lthc_ws_accumulate_bwd_workspace_bytes.argtypes = [i64, i64, ci]

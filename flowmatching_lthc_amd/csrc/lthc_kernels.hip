@@ -1971,3 +1971,5 @@ int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, cons
 #include "cast_many.inc"
 // Fused materialise backward (gdZ and gbeta from one pass over G).
 #include "materialise_bwd.inc"
+// Whole-interface entry points: recurrence prefix, read backward, interface forward / backward.
+#include "interface.inc"

@@ -386,6 +386,55 @@ int lthc_block_tail_fwd(const void* z, const void* a, const void* m, const void*
                         int64_t mod_ld, void* dz, void* z_next, void* y, int64_t B, int64_t N, int64_t C, float eps,
                         void* stream);
 
+/*
+ * RECURRENCE OVER ALL LAYERS (one pass; the all-L form of lthc_recur_fwd):
+ *   z_out[l] = Z_{l+1} = Z_l + gamma[l] * dz[l],  Z_0 = z0,  l = 0..L-1
+ * each step rounded to x_dtype as lthc_recur_fwd rounds it (bitwise equal to
+ * L calls), Z_0 read once.  gamma is [L, C] in g_dtype; dz and z_out are host
+ * arrays of L device pointers.  For callers that hold every dZ_l at once; the
+ * lazy forward of local_thc.py:1376-1385 has a branch between the steps.
+ */
+int lthc_recur_fwd_prefix(const void* z0, const void* const* dz, int x_dtype, const void* gamma, int g_dtype,
+                          void* const* z_out, int64_t rows, int64_t C, int L, void* stream);
+
+/*
+ * READ BACKWARD (autograd of SharedLocalRead.read, local_thc.py:1211-1223;
+ * jit_thc::local_read_add_traceable + local_weight_grad_traceable,
+ * local_thc_triton_kernels.py:2713-2764):
+ *   dx[cell,k,c]  = g_base[cell,k,c] + alpha[c,k] gz[cell,c]   (g_base may be NULL: zero)
+ *   dalpha[c,k]   = sum_cells x[cell,k,c] gz[cell,c]            (fp32, fixed order)
+ * dx or dalpha may be NULL to skip that output.
+ */
+size_t lthc_read_bwd_workspace_bytes(int64_t B, int64_t G, int64_t s, int64_t C);
+int lthc_read_bwd(const void* gz, const void* x, int x_dtype, const void* alpha, int w_dtype, const void* g_base,
+                  void* dx, float* dalpha, int64_t B, int64_t G, int64_t s, int64_t C, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/*
+ * WHOLE INTERFACE, every branch update given (local_thc.py:1376-1385 with the
+ * dZ_l known in advance; docs/model.md:54-108):
+ *   forward:  z[0] = R(x0); gamma_l = sum_k alpha beta_l (fp32);
+ *             z[l+1] = z[l] + gamma_l * dz[l]; x_out = x0 + sum_l P_l(dz[l])
+ *             (z holds L + 1 outputs)
+ *   backward: given gx = dL/dX_L and gz[l] = dL/dZ_l for l < L (NULL entries
+ *             are zero; Z_L feeds nothing), with S_l = sum_{j >= l} gz[j]:
+ *             dx0 = gx + R^T S_0;  ddz[l] = P_l^T gx + gamma_l S_{l+1};
+ *             dbeta[l] = sum gx dz_l + (sum S_{l+1} dz_l) alpha;
+ *             dalpha = sum x0 S_0 + sum_l (sum S_{l+1} dz_l) beta_l
+ *             (dalpha [C,16], dbeta [L,C,16] fp32; fixed-order reductions).
+ * Compositions of the per-op entry points (read, gamma, recurrence prefix,
+ * materialise; materialise backward, recurrence backward, read backward).
+ * One caller workspace of lthc_interface_workspace_bytes() serves both.
+ */
+size_t lthc_interface_workspace_bytes(int64_t B, int64_t G, int64_t s, int64_t C, int L);
+int lthc_interface_fwd(const void* x0, int x_dtype, const void* alpha, const void* const* beta, int w_dtype,
+                       const void* const* dz, void* const* z, void* x_out, int64_t B, int64_t G, int64_t s, int64_t C,
+                       int L, void* workspace, size_t workspace_bytes, void* stream);
+int lthc_interface_bwd(const void* gx, const void* const* gz, int x_dtype, const void* x0, const void* const* dz,
+                       const void* alpha, const void* const* beta, int w_dtype, void* dx0, void* const* ddz,
+                       float* dalpha, float* dbeta, int64_t B, int64_t G, int64_t s, int64_t C, int L, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

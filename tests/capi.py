@@ -2,6 +2,8 @@
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 from flowmatching_lthc_amd import _abi
@@ -130,3 +132,68 @@ def recur_bwd_sum(
     )  # fmt: skip
     _abi.check(rc, "lthc_recur_bwd_sum")
     return gsum, gdz, gg
+
+
+def recur_prefix(z0: torch.Tensor, dzs, gam: torch.Tensor) -> list[torch.Tensor]:
+    """Z_1..Z_L from lthc_recur_fwd_prefix; gam [L, C]."""
+    c = z0.shape[-1]
+    outs = [torch.empty_like(z0) for _ in dzs]
+    rc = _lib().lthc_recur_fwd_prefix(
+        z0.data_ptr(), _abi.ptr_array(dzs), _abi.code(z0), gam.data_ptr(), _abi.code(gam), _abi.ptr_array(outs),
+        z0.numel() // c, c, len(dzs), _stream(),
+    )  # fmt: skip
+    _abi.check(rc, "lthc_recur_fwd_prefix")
+    return outs
+
+
+def read_bwd(gz: torch.Tensor, x: torch.Tensor, alpha: torch.Tensor, g_base: torch.Tensor | None = None):
+    b, h, _, c = x.shape
+    g = h // S
+    dx = torch.empty_like(x)
+    da = torch.empty((c, S * S), device=x.device, dtype=torch.float32)
+    nbytes = int(_lib().lthc_read_bwd_workspace_bytes(b, g, S, c))
+    ws = torch.empty((max(nbytes, 16),), device=x.device, dtype=torch.uint8)
+    rc = _lib().lthc_read_bwd(
+        gz.data_ptr(), x.data_ptr(), _abi.code(x), alpha.data_ptr(), _abi.code(alpha), _abi.ptr(g_base),
+        dx.data_ptr(), da.data_ptr(), b, g, S, c, ws.data_ptr(), ws.numel(), _stream(),
+    )  # fmt: skip
+    _abi.check(rc, "lthc_read_bwd")
+    return dx, da
+
+
+def _iface_ws(b, g, c, L, dev):
+    nbytes = int(_lib().lthc_interface_workspace_bytes(b, g, S, c, L))
+    return torch.empty((max(nbytes, 16),), device=dev, dtype=torch.uint8)
+
+
+def interface_fwd(x0: torch.Tensor, alpha: torch.Tensor, betas, dzs):
+    b, h, _, c = x0.shape
+    g, L = h // S, len(dzs)
+    zs = [torch.empty((b, g * g, c), device=x0.device, dtype=x0.dtype) for _ in range(L + 1)]
+    xl = torch.empty_like(x0)
+    ws = _iface_ws(b, g, c, L, x0.device)
+    rc = _lib().lthc_interface_fwd(
+        x0.data_ptr(), _abi.code(x0), alpha.data_ptr(), _abi.ptr_array(betas), _abi.code(betas[0]),
+        _abi.ptr_array(dzs), _abi.ptr_array(zs), xl.data_ptr(), b, g, S, c, L, ws.data_ptr(), ws.numel(), _stream(),
+    )  # fmt: skip
+    _abi.check(rc, "lthc_interface_fwd")
+    return zs, xl
+
+
+def interface_bwd(gx: torch.Tensor, gzs, x0: torch.Tensor, dzs, alpha: torch.Tensor, betas):
+    """gzs: L entries (None = zero).  Returns (dx0, [ddz_l], dalpha fp32 [C,16], dbeta fp32 [L,C,16])."""
+    b, h, _, c = x0.shape
+    g, L = h // S, len(dzs)
+    dx0 = torch.empty_like(x0)
+    ddz = [torch.empty_like(d) for d in dzs]
+    da = torch.empty((c, S * S), device=x0.device, dtype=torch.float32)
+    db = torch.empty((L, c, S * S), device=x0.device, dtype=torch.float32)
+    ws = _iface_ws(b, g, c, L, x0.device)
+    gz_ptrs = (ctypes.c_void_p * L)(*[None if t is None else t.data_ptr() for t in gzs])
+    rc = _lib().lthc_interface_bwd(
+        gx.data_ptr(), gz_ptrs, _abi.code(x0), x0.data_ptr(), _abi.ptr_array(dzs), alpha.data_ptr(),
+        _abi.ptr_array(betas), _abi.code(betas[0]), dx0.data_ptr(), _abi.ptr_array(ddz), da.data_ptr(), db.data_ptr(),
+        b, g, S, c, L, ws.data_ptr(), ws.numel(), _stream(),
+    )  # fmt: skip
+    _abi.check(rc, "lthc_interface_bwd")
+    return dx0, ddz, da, db

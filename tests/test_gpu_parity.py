@@ -586,3 +586,89 @@ def test_norm_modulate_forward_and_backward(dtype, C):
     ya.backward(gy)
     assert torch.equal(xa.grad, gx) and torch.equal(wa.grad, gw.to(wa.dtype))
     assert torch.equal(sha.grad, gsh.to(dtype)) and torch.equal(sca.grad, gsc.to(dtype))
+
+
+# ---------------------------------------------------------------------------
+# whole-interface entry points: recurrence prefix, read backward, interface fwd / bwd
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("xdt", [F32, BF16, torch.float16])
+@pytest.mark.parametrize("C,L", [(768, 12), (768, 1), (260, 5)])
+def test_recurrence_prefix_equals_single_steps(xdt, C, L):
+    """lthc_recur_fwd_prefix: Z_1..Z_L bitwise equal to L lthc_recur_fwd launches (C = 260 takes the per-step
+    path, the others the one-pass kernel), gamma fp32 or in the activation dtype."""
+    print(f"case x={xdt} C={C} L={L}", flush=True)
+    d = cfg(2, 16, C, L, seed=C + L, grads=True)
+    z0 = dev(d["grad_z"][0] * 50.0, xdt)
+    dzs = [dev(z, xdt) for z in d["dz"]]
+    for gdt in (F32, xdt):
+        gam = dev(np.stack([d["alpha"][:, l % 16] * 3.0 for l in range(L)]), gdt)
+        got = capi.recur_prefix(z0, dzs, gam)
+        z = z0
+        for l in range(L):
+            z = capi.recur(z, dzs[l], gam[l])
+            assert torch.equal(got[l], z), f"Z_{l + 1} differs from the single steps"
+
+
+def test_read_backward_entry():
+    """lthc_read_bwd: dx = g_base + R^T gz (and without a base), dalpha = sum x gz, against the oracle (fp32)."""
+    d = cfg(2, 16, 256, 1, seed=9, grads=True)
+    x, gz, alpha, base = dev(d["x0"]), dev(d["grad_z"][0]), dev(d["alpha"]), dev(d["grad_xl"])
+    dx, da = capi.read_bwd(gz, x, alpha, base)
+    ref = O.write_np(d["grad_z"][0], d["alpha"], 64) + np.asarray(d["grad_xl"], np.float64)
+    assert_f32(host(dx), ref, what="dx with base")
+    assert_f32(host(da), O.weight_grad_np(d["x0"], d["grad_z"][0], 16), what="dalpha")
+    dx0, _ = capi.read_bwd(gz, x, alpha)
+    assert_f32(host(dx0), O.write_np(d["grad_z"][0], d["alpha"], 64), what="dx without base")
+
+
+@pytest.mark.parametrize("missing", [(), (0,), (2,), (1, 2, 3)])
+def test_interface_entry_points_match_closed_form_fp32(missing):
+    """lthc_interface_fwd against read / gamma / recurrence / materialise in float64, lthc_interface_bwd against the
+    closed-form backward (oracle.interface_bwd_np); `missing` workspace gradients are passed as NULL (zero)."""
+    print(f"case missing={missing}", flush=True)
+    B, G, C, L = 2, 16, 64, 4
+    d = cfg(B, G, C, L, seed=17, grads=True)
+    x0, alpha = dev(d["x0"]), dev(d["alpha"])
+    betas, dzs = [dev(b) for b in d["beta"]], [dev(z) for z in d["dz"]]
+    zs, xl = capi.interface_fwd(x0, alpha, betas, dzs)
+    z = O.read_np(d["x0"], d["alpha"], G)
+    assert_f32(host(zs[0]), z, what="Z_0")
+    for l in range(L):
+        z = z + O.gamma_np(d["alpha"], d["beta"][l])[None, None, :] * np.asarray(d["dz"][l], np.float64)
+        assert_f32(host(zs[l + 1]), z, what=f"Z_{l + 1}")
+    xref = np.asarray(d["x0"], np.float64)
+    for l in range(L):
+        xref = xref + O.write_np(d["dz"][l], d["beta"][l], 4 * G)
+    assert_f32(host(xl), xref, what="X_L")
+    gz_np = [np.zeros_like(np.asarray(g)) if l in missing else g for l, g in enumerate(d["grad_z"])]
+    gzs = [None if l in missing else dev(g) for l, g in enumerate(d["grad_z"])]
+    dx0, ddz, da, db = capi.interface_bwd(dev(d["grad_xl"]), gzs, x0, dzs, alpha, betas)
+    ref = O.interface_bwd_np(d["x0"], d["alpha"], list(d["dz"]), list(d["beta"]), d["grad_xl"], gz_np, G)
+    assert_f32(host(dx0), ref["x0"], what="dX0")
+    assert_f32(host(da), ref["alpha"], what="dalpha")
+    for l in range(L):
+        assert_f32(host(ddz[l]), ref["dz"][l], what=f"d dZ_{l}")
+        assert_f32(host(db[l]), ref["beta"][l], what=f"dbeta_{l}")
+
+
+def test_interface_entry_points_bf16_configuration3_slice(coracle):
+    """The whole-interface entry points at configuration 3's width and depth (B=4 slice, bf16, fp32 weights):
+    X_L within one bf16 rounding of the oracle, gradients to the bf16 bar."""
+    B, G, C, L = 4, 16, 768, 12
+    d = cfg(B, G, C, L, seed=23, grads=True)
+    x0, alpha = dev(d["x0"], BF16), dev(d["alpha"])
+    betas, dzs = [dev(b) for b in d["beta"]], [dev(z, BF16) for z in d["dz"]]
+    zs, xl = capi.interface_fwd(x0, alpha, betas, dzs)
+    x0h, dzh = host(x0), [host(z) for z in dzs]
+    assert_bf16(host(xl), coracle.Cwrite(x0h, dzh, list(d["beta"])), what="X_L")
+    assert_bf16(host(zs[0]), coracle.Cread(x0h, d["alpha"], G), what="Z_0")
+    gx, gzs = dev(d["grad_xl"], BF16), [dev(g, BF16) for g in d["grad_z"]]
+    dx0, ddz, da, db = capi.interface_bwd(gx, gzs, x0, dzs, alpha, betas)
+    ref = O.interface_bwd_np(x0h, d["alpha"], dzh, list(d["beta"]), host(gx), [host(g) for g in gzs], G)
+    assert np.abs(host(dx0) - ref["x0"]).max() <= 2e-2
+    for l in range(L):
+        assert np.abs(host(ddz[l]) - ref["dz"][l]).max() <= 2e-2, l
+    # weight gradients sum bf16-rounded suffix sums over 1024 cells: relative to their scale
+    for got, r, what in [(host(da), ref["alpha"], "dalpha")] + [(host(db[l]), ref["beta"][l], f"dbeta_{l}") for l in range(L)]:
+        err = np.abs(got - r).max() / max(np.abs(r).max(), 1e-30)
+        assert err <= 2e-2, f"{what}: {err:.3e}"
