@@ -319,6 +319,87 @@ def interface_forward(args, torch, dev, ops, B, G, C, L):
     }
 
 
+def interface_c_level(args, torch, dev, B, G, C, L):
+    """The whole-interface C entry points with every dZ_l given (lthc_interface_fwd, lthc_interface_bwd): one call
+    each, no autograd, events around `steps` calls over two input sets.  Not the metric's step (the model's lazy
+    forward runs a branch between the recurrence steps); reported beside it.  Bytes: forward e(3T + (3L + 2)W)
+    (read, prefix recurrence e(W + 2LW), materialise); backward e(4T + 8LW + W) as interface_train counts it."""
+    from flowmatching_lthc_amd import _abi
+
+    lib = _abi.load()
+    H = 4 * G
+    bf16 = torch.bfloat16
+    gen = torch.Generator(device=dev).manual_seed(13)
+    alpha = torch.randn((C, 16), generator=gen, device=dev) * 0.01 + 1.0 / 16.0
+    betas = [torch.randn((C, 16), generator=gen, device=dev) * 0.02 for _ in range(L)]
+    sets = []
+    for _ in range(2):
+        x0 = torch.randn((B, H, H, C), generator=gen, device=dev).to(bf16)
+        dzs = [(torch.randn((B, G * G, C), generator=gen, device=dev) * 0.02).to(bf16) for _ in range(L)]
+        sets.append((x0, dzs, _abi.ptr_array(dzs)))
+    zs = [torch.empty((B, G * G, C), device=dev, dtype=bf16) for _ in range(L + 1)]
+    xl = torch.empty((B, H, H, C), device=dev, dtype=bf16)
+    nbytes = int(lib.lthc_interface_workspace_bytes(B, G, 4, C, L))
+    ws = torch.empty((max(nbytes, 16),), device=dev, dtype=torch.uint8)
+    stream = torch.cuda.current_stream()
+    sid = stream.cuda_stream
+    bp, zp = _abi.ptr_array(betas), _abi.ptr_array(zs)
+
+    def fwd(i):
+        x0, _, dzp = sets[i & 1]
+        _abi.check(lib.lthc_interface_fwd(
+            x0.data_ptr(), _abi.code(x0), alpha.data_ptr(), bp, _abi.code(alpha), dzp, zp, xl.data_ptr(), B, G, 4, C,
+            L, ws.data_ptr(), ws.numel(), sid,
+        ), "lthc_interface_fwd")  # fmt: skip
+
+    gx = (torch.randn((B, H, H, C), generator=gen, device=dev) * 1e-3).to(bf16)
+    gzs = [(torch.randn((B, G * G, C), generator=gen, device=dev) * 1e-3).to(bf16) for _ in range(L)]
+    dx0 = torch.empty_like(gx)
+    ddz = [torch.empty((B, G * G, C), device=dev, dtype=bf16) for _ in range(L)]
+    da = torch.empty((C, 16), device=dev, dtype=torch.float32)
+    db = torch.empty((L, C, 16), device=dev, dtype=torch.float32)
+    gzp, ddzp = _abi.ptr_array(gzs), _abi.ptr_array(ddz)
+
+    def bwd(i):
+        x0, _, dzp = sets[i & 1]
+        _abi.check(lib.lthc_interface_bwd(
+            gx.data_ptr(), gzp, _abi.code(gx), x0.data_ptr(), dzp, alpha.data_ptr(), bp,
+            _abi.code(alpha), dx0.data_ptr(), ddzp, da.data_ptr(), db.data_ptr(), B, G, 4, C, L,
+            ws.data_ptr(), ws.numel(), sid,
+        ), "lthc_interface_bwd")  # fmt: skip
+
+    def timed(fn):
+        for i in range(args.warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(args.steps):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / args.steps
+
+    fwd_ms, bwd_ms = timed(fwd), timed(bwd)
+    T, W = B * H * H * C, B * G * G * C
+    fb = 2 * (3 * T + (3 * L + 2) * W)
+    bb = 2 * (4 * T + 8 * L * W + W)
+    out = {
+        "workload": f"whole-interface C calls, every dZ_l given (B={B}, {H}x{H}/{G}x{G}, C={C}, L={L}, bf16, fp32 weights)",
+        "timing": "events around consecutive calls, eager (several launches per call)",
+        "fwd_ms": round(fwd_ms, 4),
+        "fwd_bytes": fb,
+        "fwd_GBps": round(fb / (fwd_ms * 1e-3) / 1e9, 1),
+        "bwd_ms": round(bwd_ms, 4),
+        "bwd_per_op_bytes": bb,
+        "bwd_per_op_GBps": round(bb / (bwd_ms * 1e-3) / 1e9, 1),
+    }
+    del sets, zs, xl, ws, gx, gzs, dx0, ddz
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def triangular_forward(args, torch, dev, B, G, C, L):
     """The non-shared (triangular lazy) interface forward at one shape: the L bases R_l(x0) in one pass
     (jit_thc::all_base_b4_12_split_traceable), the L-1 workspace sums z_l = base_l + sum_{j<l} gamma[l,j] dz_j
@@ -708,6 +789,8 @@ def main():
             "config5_fwd": interface_forward(args, torch, dev, ops, 32, 32, 1024, 24),
             "config5_train": interface_train(args, torch, dev, ops, 32, 32, 1024, 24, label="configuration 5"),
             "triangular_fwd_metric_shape": triangular_forward(args, torch, dev, B, G, C, L),
+            "interface_c_level_metric_shape": interface_c_level(args, torch, dev, B, G, C, L),
+            "interface_c_level_config3": interface_c_level(args, torch, dev, args.train_batch, G, C, L),
         }
 
     cpu = None
