@@ -621,13 +621,24 @@ def test_read_backward_entry():
     assert_f32(host(dx0), O.write_np(d["grad_z"][0], d["alpha"], 64), what="dx without base")
 
 
-@pytest.mark.parametrize("missing", [(), (0,), (2,), (1, 2, 3)])
-def test_interface_entry_points_match_closed_form_fp32(missing):
+@pytest.mark.parametrize(
+    "B,G,C,L,missing",
+    [
+        (2, 16, 64, 4, ()),
+        (2, 16, 64, 4, (0,)),
+        (2, 16, 64, 4, (2,)),
+        (2, 16, 64, 4, (1, 2, 3)),
+        # C % 64 != 0 and depth 26 > 24: the materialise backward and the recurrence prefix take their
+        # per-layer fallbacks; an 8x8 workspace (32x32 grid) and a 32x32 one (128x128 grid)
+        (1, 8, 72, 26, (5,)),
+        (1, 32, 64, 2, ()),
+    ],
+)
+def test_interface_entry_points_match_closed_form_fp32(B, G, C, L, missing):
     """lthc_interface_fwd against read / gamma / recurrence / materialise in float64, lthc_interface_bwd against the
     closed-form backward (oracle.interface_bwd_np); `missing` workspace gradients are passed as NULL (zero)."""
-    print(f"case missing={missing}", flush=True)
-    B, G, C, L = 2, 16, 64, 4
-    d = cfg(B, G, C, L, seed=17, grads=True)
+    print(f"case B={B} G={G} C={C} L={L} missing={missing}", flush=True)
+    d = cfg(B, G, C, L, seed=17 + C + L, grads=True)
     x0, alpha = dev(d["x0"]), dev(d["alpha"])
     betas, dzs = [dev(b) for b in d["beta"]], [dev(z) for z in d["dz"]]
     zs, xl = capi.interface_fwd(x0, alpha, betas, dzs)
