@@ -423,7 +423,10 @@ int lthc_read_bwd(const void* gz, const void* x, int x_dtype, const void* alpha,
  *             dalpha = sum x0 S_0 + sum_l (sum S_{l+1} dz_l) beta_l
  *             (dalpha [C,16], dbeta [L,C,16] fp32; fixed-order reductions).
  * Compositions of the per-op entry points (read, gamma, recurrence prefix,
- * materialise; materialise backward, recurrence backward, read backward).
+ * materialise; materialise backward, read backward); up to depth 24 the
+ * backward's recurrence steps run in one pass over H, dZ and gdZ, giving the
+ * per-step entry points' values bit for bit (one lthc_recur_bwd or
+ * lthc_recur_bwd_sum per step above that depth).
  * One caller workspace of lthc_interface_workspace_bytes() serves both.
  */
 size_t lthc_interface_workspace_bytes(int64_t B, int64_t G, int64_t s, int64_t C, int L);

@@ -662,6 +662,53 @@ def test_interface_entry_points_match_closed_form_fp32(B, G, C, L, missing):
         assert_f32(host(db[l]), ref["beta"][l], what=f"dbeta_{l}")
 
 
+@pytest.mark.parametrize("xdt", [BF16, torch.float16, F32])
+@pytest.mark.parametrize(
+    "L,missing",
+    [(12, ()), (12, (0, 11)), (12, (3, 4, 5)), (5, (2,)), (24, (7,)), (3, (1, 2))],
+)
+def test_interface_bwd_one_pass_suffix_equals_per_step_chain(xdt, L, missing):
+    """lthc_interface_bwd walks the recurrence backward of every step in one pass (recur_suffix_kernel, depth <= 24).
+    Its dZ gradients and dX0 equal, bit for bit, the chain of per-step entry points it replaces: materialise
+    backward, then l = L-1..0 one lthc_recur_bwd / lthc_recur_bwd_sum on the running suffix sum S_{l+1}, then
+    S_0 = r(S_1 + H_0) and lthc_read_bwd.  The weight gradients sum in another order (relative 1e-5)."""
+    print(f"case x={xdt} L={L} missing={missing}", flush=True)
+    B, G, C = 2, 16, 256
+    d = cfg(B, G, C, L, seed=31 + L, grads=True)
+    x0, alpha = dev(d["x0"], xdt), dev(d["alpha"])
+    betas, dzs = [dev(b) for b in d["beta"]], [dev(z, xdt) for z in d["dz"]]
+    gx = dev(d["grad_xl"], xdt)
+    gzs = [None if l in missing else dev(g, xdt) for l, g in enumerate(d["grad_z"])]
+    dx0, ddz, da, db = capi.interface_bwd(gx, gzs, x0, dzs, alpha, betas)
+
+    gam = capi.gamma(alpha, betas)
+    ref_dz, ref_db = capi.materialise_bwd(gx, dzs, betas)
+    gg = [torch.zeros((C,), device=DEV) for _ in range(L)]
+    cur = None
+    for l in reversed(range(L)):
+        h = gzs[l + 1] if l + 1 < L else None
+        if cur is None and h is None:
+            continue
+        if cur is not None and h is not None:
+            cur, ref_dz[l], gg[l] = capi.recur_bwd_sum(cur, h, dzs[l], gam[l], add=ref_dz[l])
+        else:
+            cur = cur if cur is not None else h
+            ref_dz[l], gg[l] = capi.recur_bwd(cur, dzs[l], gam[l], add=ref_dz[l])
+    if gzs[0] is not None:
+        cur = gzs[0] if cur is None else (cur.float() + gzs[0].float()).to(xdt)
+    assert cur is not None
+    ref_dx0, ref_da = capi.read_bwd(cur, x0, alpha, gx)
+    for l in range(L):
+        assert torch.equal(ddz[l], ref_dz[l]), f"d dZ_{l}: {(ddz[l] != ref_dz[l]).float().mean().item():.2e} differ"
+    assert torch.equal(dx0, ref_dx0)
+    a = alpha.float()
+    ref_da = ref_da + sum(gg[l][:, None] * betas[l] for l in range(L))
+    ref_db = torch.stack([ref_db[l] + gg[l][:, None] * a for l in range(L)])
+    for got, ref, what in ((da, ref_da, "dalpha"), (db, ref_db, "dbeta")):
+        err = ((got - ref).abs().max() / ref.abs().max()).item()
+        assert err <= 1e-5, f"{what}: {err:.3e}"
+
+
 def test_interface_entry_points_bf16_configuration3_slice(coracle):
     """The whole-interface entry points at configuration 3's width and depth (B=4 slice, bf16, fp32 weights):
     X_L within one bf16 rounding of the oracle, gradients to the bf16 bar."""
