@@ -323,7 +323,8 @@ def interface_c_level(args, torch, dev, B, G, C, L):
     """The whole-interface C entry points with every dZ_l given (lthc_interface_fwd, lthc_interface_bwd): one call
     each, no autograd, events around `steps` calls over two input sets.  Not the metric's step (the model's lazy
     forward runs a branch between the recurrence steps); reported beside it.  Bytes: forward e(3T + (3L + 2)W)
-    (read, prefix recurrence e(W + 2LW), materialise); backward e(4T + 8LW + W) as interface_train counts it."""
+    (read, prefix recurrence e(W + 2LW), materialise); backward e(4T + 6LW + 3W): materialise backward e(T + 2LW),
+    the one-pass recurrence backward e(4LW + W), the read backward's dX0 e(2T + W) and dalpha e(T + W)."""
     from flowmatching_lthc_amd import _abi
 
     lib = _abi.load()
@@ -383,7 +384,7 @@ def interface_c_level(args, torch, dev, B, G, C, L):
     fwd_ms, bwd_ms = timed(fwd), timed(bwd)
     T, W = B * H * H * C, B * G * G * C
     fb = 2 * (3 * T + (3 * L + 2) * W)
-    bb = 2 * (4 * T + 8 * L * W + W)
+    bb = 2 * (4 * T + 6 * L * W + 3 * W)
     out = {
         "workload": f"whole-interface C calls, every dZ_l given (B={B}, {H}x{H}/{G}x{G}, C={C}, L={L}, bf16, fp32 weights)",
         "timing": "events around consecutive calls, eager (several launches per call)",
@@ -391,8 +392,8 @@ def interface_c_level(args, torch, dev, B, G, C, L):
         "fwd_bytes": fb,
         "fwd_GBps": round(fb / (fwd_ms * 1e-3) / 1e9, 1),
         "bwd_ms": round(bwd_ms, 4),
-        "bwd_per_op_bytes": bb,
-        "bwd_per_op_GBps": round(bb / (bwd_ms * 1e-3) / 1e9, 1),
+        "bwd_bytes": bb,
+        "bwd_GBps": round(bb / (bwd_ms * 1e-3) / 1e9, 1),
     }
     del sets, zs, xl, ws, gx, gzs, dx0, ddz
     torch.cuda.synchronize()
