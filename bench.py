@@ -56,11 +56,14 @@ def parse_args():
     p.add_argument("--no-configs", action="store_true", help="skip the BASELINE configuration 2 and 5 legs")
     p.add_argument(
         "--profile",
-        choices=["materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model", "train", "triangular"],
+        choices=[
+            "materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model", "train", "triangular",
+            "interface_c",
+        ],  # fmt: skip
         help="run only this kernel --steps times at the configured shape (for rocprofv3), plus one plain copy "
         "of X0 (a copy kernel of known size that calibrates the FETCH_SIZE / WRITE_SIZE counters); 'model' runs "
         "only the LTHC-B/4 forward leg (without the eager-interface comparison), 'train' only the interface fwd+bwd leg, 'triangular' only the non-shared "
-        "interface forward leg",
+        "interface forward leg, 'interface_c' only the whole-interface C calls at the training batch",
     )
     return p.parse_args()
 
@@ -673,6 +676,10 @@ def main():
         return
     if args.profile == "train":
         print(json.dumps({"interface_train": interface_train(args, torch, dev, ops)}))
+        return
+    if args.profile == "interface_c":  # the whole-interface C calls at the training batch (configuration 3)
+        leg = interface_c_level(args, torch, dev, args.train_batch, args.grid, args.channels, args.depth)
+        print(json.dumps({"interface_c_level": leg}))
         return
     if args.profile == "triangular":
         tri = triangular_forward(args, torch, dev, args.batch, args.grid, args.channels, args.depth)
