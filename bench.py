@@ -53,7 +53,7 @@ def parse_args():
     p.add_argument("--no-model", action="store_true", help="skip the LTHC-B/4 forward leg")
     p.add_argument("--train-batch", type=int, default=64, help="batch of the interface fwd+bwd leg (configuration 3)")
     p.add_argument("--no-train", action="store_true", help="skip the interface fwd+bwd leg")
-    p.add_argument("--no-configs", action="store_true", help="skip the BASELINE configuration 2 and 5 legs")
+    p.add_argument("--no-configs", action="store_true", help="skip the benchmark configuration 2 and 5 legs")
     p.add_argument(
         "--profile",
         choices=[
@@ -97,7 +97,7 @@ def cpu_baseline(G, C, L, budget_s):
         O.build()
     threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
     O.set_threads(threads)
-    Bs = 32  # the batch of BASELINE configuration 2
+    Bs = 32  # the batch of benchmark configuration 2
     d = O.make_inputs(Bs, G, C, L, seed=0)
     x0, alpha = d["x0"], d["alpha"]
     betas, dzs = list(d["beta"]), list(d["dz"])
@@ -506,7 +506,7 @@ def triangular_forward(args, torch, dev, B, G, C, L):
 
 
 def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label="configuration 3"):
-    """the interface forward + autograd backward at the training shape (B=64, bf16).
+    """Benchmark configuration 3: the interface forward + autograd backward at the training shape (B=64, bf16).
 
     X0, alpha, the 12 beta_l and the 12 dZ_l are leaves that require grad; the upstream gradients are
     G_L = dL/dX_L ~ N(0, 1e-3) and H_l = dL/dZ_l ~ N(0, 1e-3) for the 12 workspace states Z_0..Z_11 that feed

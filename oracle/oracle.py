@@ -323,7 +323,7 @@ def Crecur_bwd(gr, dz, gamma):
 
 
 # ---------------------------------------------------------------------------
-# Seeded inputs of the BASELINE configurations (one CPU torch.Generator, fixed
+# Seeded inputs of the benchmark configurations (one CPU torch.Generator, fixed
 # draw order: X0, alpha, beta stack, dZ stack, then upstream gradients)
 # ---------------------------------------------------------------------------
 def make_inputs(B: int, G: int, C: int, L: int, seed: int = 0, grads: bool = False, S: int = 4):
