@@ -17,8 +17,9 @@ input once and writes each output once; e = 2, T = B*64*64*C, W = B*256*C).
 
 Prints one JSON line.  `roofline` covers the dominant kernel (the
 materialisation), timed with HIP events around each of its launches on the
-stream it runs on; `cpu_baseline` times the C oracle (oracle/lthc_oracle.c,
-OpenMP) on a bounded slice of the same workload on the host cores.
+stream it runs on; `cpu_baseline` times the reference's eager PyTorch op
+sequence for the same step (oracle/torch_cpu.py, fp32 CPU tensors) at the
+metric shape on the host cores this process may use.
 """
 
 from __future__ import annotations
@@ -34,6 +35,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 METRIC = "read/write/materialise HBM GB/s (% of 8 TB/s) at B=256 C=768 bf16; fwd img/s"
 PEAK_HBM = 8.0e12
 PMC_PROFILE = os.path.join(ROOT, "profiles", "materialise_fwd_b256_pmc.txt")
+KERNEL_SOURCE = os.path.join(ROOT, "flowmatching_lthc_amd", "csrc", "lthc_kernels.hip")
 
 
 def parse_args():
@@ -46,7 +48,7 @@ def parse_args():
     p.add_argument("--depth", type=int, default=12)
     p.add_argument("--grid", type=int, default=16, help="workspace grid side (high-res side = 4x)")
     p.add_argument("--mode", choices=["graph", "eager"], default="graph", help="how `value` is timed")
-    p.add_argument("--cpu-seconds", type=float, default=12.0, help="budget of the CPU baseline sample")
+    p.add_argument("--cpu-seconds", type=float, default=20.0, help="budget of the CPU baseline's metric-shape sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--model-batch", type=int, default=64, help="batch of the LTHC-B/4 forward leg (fwd img/s)")
     p.add_argument("--model-steps", type=int, default=10)
@@ -78,16 +80,114 @@ def algorithmic_bytes(B, G, C, L, e=2):
     return {"read": read, "gamma": gamma, "recur": recur, "materialise": mat, "total": read + gamma + recur + mat}
 
 
+def kernel_source_sha1():
+    """sha1 of the source file that holds the materialise kernel (the PMC summary records the one it measured)."""
+    import hashlib
+
+    return hashlib.sha1(open(KERNEL_SOURCE, "rb").read()).hexdigest()
+
+
 def pmc_traffic():
-    """HBM bytes per materialise launch from the committed rocprofv3 --pmc summary, if any."""
+    """HBM bytes per materialise launch from the committed rocprofv3 --pmc summary, and where the figure comes
+    from.  The figure is None when the summary is missing or was measured on another kernel source than the one
+    built now (its recorded kernel_source_sha1 differs): counters are not collected inside this run."""
+    rel_path = os.path.relpath(PMC_PROFILE, ROOT)
     if not os.path.exists(PMC_PROFILE):
-        return None
-    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", open(PMC_PROFILE).read())
-    return float(m.group(1)) if m else None
+        return None, f"no committed PMC summary ({rel_path})"
+    text = open(PMC_PROFILE).read()
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", text)
+    h = re.search(r"kernel_source_sha1:\s*([0-9a-f]+)", text)
+    if m is None:
+        return None, f"{rel_path} holds no traffic figure"
+    if h is None or h.group(1) != kernel_source_sha1():
+        return None, f"{rel_path} was measured on another kernel source than this build's: not reported"
+    return float(m.group(1)), f"committed rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this kernel source ({rel_path}); not measured in this run"
 
 
-def cpu_baseline(G, C, L, budget_s):
-    """The C oracle on a slice of the same workload (fp32, OpenMP on the host cores)."""
+def host_cpu():
+    """(model name, logical CPUs of the host, CPUs this process may run on)."""
+    name = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    name = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return name, os.cpu_count() or 1, len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(B, G, C, L, budget_s):
+    """The reference's eager PyTorch op sequence (oracle/torch_cpu.py: SharedLocalRead.read local_thc.py:1211-1223,
+    lazy_workspace_update :1325-1328, the write_add loop :1368-1372) on CPU tensors in fp32, at configuration 2
+    (B=32, one warm-up step) and then at the metric shape, median time per step.  Threads: the CPUs this process
+    may use, capped by OMP_NUM_THREADS (the GPU box's share of its host)."""
+    import torch
+
+    sys.path.insert(0, ROOT)
+    from oracle import torch_cpu as TC
+
+    model, ncpu, share = host_cpu()
+    env = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(share, env) if env > 0 else share
+    prev = torch.get_num_threads()
+    torch.set_num_threads(threads)
+
+    def leg(Bs, budget, max_steps, warm):
+        gen = torch.Generator().manual_seed(0)
+        H = 4 * G
+        x0 = torch.randn((Bs, H, H, C), generator=gen)
+        alpha = torch.randn((C, 16), generator=gen) * 0.01 + 1.0 / 16.0
+        betas = [torch.randn((C, 16), generator=gen) * 0.02 for _ in range(L)]
+        dzs = [torch.randn((Bs, G * G, C), generator=gen) * 0.02 for _ in range(L)]
+        with torch.no_grad():
+            if warm:
+                TC.step(x0, alpha, betas, dzs, G)  # warm-up (allocator, thread pool)
+            times, t_start = [], time.perf_counter()
+            while len(times) < max_steps and (not times or time.perf_counter() - t_start < budget):
+                t0 = time.perf_counter()
+                TC.step(x0, alpha, betas, dzs, G)
+                times.append(time.perf_counter() - t0)
+        times.sort()
+        dt = times[len(times) // 2]
+        nbytes = algorithmic_bytes(Bs, G, C, L)["total"]
+        return {
+            "B": Bs,
+            "ms_per_step": round(dt * 1e3, 1),
+            "steps_timed": len(times),
+            "GBps": round(nbytes / dt / 1e9, 3),
+        }
+
+    try:  # configuration 2 first: its warm-up step also warms the thread pool for the metric shape's steps
+        conf2 = leg(32, max(2.0, budget_s / 4), 10, True)
+        metric = leg(B, budget_s, 3, False)
+    finally:
+        torch.set_num_threads(prev)
+    return {
+        "value": metric["GBps"],
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": (
+            f"the reference's eager PyTorch op sequence for the interface (read local_thc.py:1211-1223, {L} "
+            f"lazy_workspace_update steps :1325-1328, the write_add loop :1368-1372; oracle/torch_cpu.py) on CPU "
+            f"tensors in fp32 at the metric shape B={B} ({metric['steps_timed']} timed step(s) after configuration 2's "
+            f"warm-up, median {metric['ms_per_step']} ms); value = the metric's bf16 algorithmic bytes / that time; "
+            f"torch.set_num_threads({threads}) on a host of {ncpu} logical CPUs ({model}), {share} of them "
+            f"available to this process"
+        ),
+        "ms_per_step": metric["ms_per_step"],
+        "host_cpu_model": model,
+        "host_logical_cpus": ncpu,
+        "threads": threads,
+        "configuration2": conf2,
+    }
+
+
+def c_oracle_baseline(G, C, L, budget_s):
+    """The C oracle (fp32 in/out, fp64 accumulate, OpenMP) on a configuration-2 slice of the workload: a secondary
+    CPU figure beside the reference's op sequence."""
     sys.path.insert(0, ROOT)
     import numpy as np
 
@@ -95,7 +195,9 @@ def cpu_baseline(G, C, L, budget_s):
 
     if not os.path.exists(O.LIB):
         O.build()
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or min(16, os.cpu_count() or 1)
+    share = len(os.sched_getaffinity(0))
+    env = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
+    threads = min(share, env) if env > 0 else share
     O.set_threads(threads)
     Bs = 32  # the batch of benchmark configuration 2
     d = O.make_inputs(Bs, G, C, L, seed=0)
@@ -121,14 +223,13 @@ def cpu_baseline(G, C, L, budget_s):
     return {
         "value": round(nbytes / dt / 1e9, 3),
         "unit": "GB/s",
-        "cores": threads,
-        "kind": "port",
+        "threads": threads,
         "sample": (
             f"C oracle (oracle/lthc_oracle.c, fp32 in/out, fp64 accumulate, OpenMP {threads} threads) running the same "
             f"step (read, gamma, {L} recurrence steps, materialise) on a B={Bs} slice of the workload; {n} steps in "
             f"{dt * n:.1f} s; value = the bf16 algorithmic bytes of that slice / time per step"
         ),
-        "ms_per_step_sample": round(dt * 1e3, 3),
+        "ms_per_step": round(dt * 1e3, 3),
     }
 
 
@@ -628,6 +729,50 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
     }
 
 
+def recurrence_cache_leg(args, torch, ops, sets, alpha, beta_stack, L, W, step_ms, step_bytes):
+    """The step's L recurrence launches timed one by one with events, as they run in the step (Z_l written by the
+    previous launch just before: served partly from the 256 MB MALL) and with Z_l and dZ_l evicted first (an
+    untimed 1 GiB streaming fill before each launch, as a transformer branch between the steps would).  Reports
+    both rates and the step time the cold launches imply: step_ms + sum_l (cold_l - warm_l)."""
+    stream = torch.cuda.current_stream()
+    flush = torch.empty((1 << 30) // 4, device=sets[0][0].device, dtype=torch.float32)
+    reps = max(2, min(args.steps, 10))
+
+    def run(cold):
+        ev = []
+        for i in range(reps):
+            x0, dzs = sets[i % 2]
+            z = ops.local_write_traceable(x0, alpha)
+            gam = ops.lazy_gamma_stack(alpha, beta_stack)
+            for l in range(L):
+                if cold:
+                    flush.fill_(float(l))
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record(stream)
+                z = ops.lazy_workspace_update(z, dzs[l], gam[l])
+                e1.record(stream)
+                ev.append((e0, e1))
+        torch.cuda.synchronize()
+        return sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+
+    run(True)  # warm-up of both paths
+    warm_ms, cold_ms = run(False), run(True)
+    del flush
+    rb = 2 * 3 * W  # bytes per launch: Z_l and dZ_l in, Z_{l+1} out (bf16; gamma negligible)
+    cold_step = step_ms + L * (cold_ms - warm_ms)
+    return {
+        "per_launch_us_in_step_order": round(warm_ms * 1e3, 2),
+        "per_launch_GBps_in_step_order": round(rb / (warm_ms * 1e-3) / 1e9, 1),
+        "per_launch_us_mall_cold": round(cold_ms * 1e3, 2),
+        "per_launch_GBps_mall_cold": round(rb / (cold_ms * 1e-3) / 1e9, 1),
+        "step_ms_implied_mall_cold": round(cold_step, 4),
+        "pct_of_peak_hbm_implied_mall_cold": round(100.0 * step_bytes / (cold_step * 1e-3) / PEAK_HBM, 2),
+        "note": "the headline value times the step as launched back to back, where each recurrence launch reads the "
+        "Z_l that the previous launch wrote microseconds earlier; with a branch between the steps (the model) Z_l "
+        "comes from HBM: this leg evicts it with a 1 GiB fill before every launch",
+    }
+
+
 def profile(args, ops, inputs, alpha, beta_stack, betas):
     """One kernel, --warmup + --steps launches, then a plain copy of X0 (bytes known: 2 x X0)."""
     import torch
@@ -778,7 +923,8 @@ def main():
     nbytes = algorithmic_bytes(B, G, C, L)
     value = nbytes["total"] / (ms * 1e-3) / 1e9
     mat_achieved = nbytes["materialise"] / (mat_ms * 1e-3)
-    traffic = pmc_traffic()
+    traffic, traffic_source = pmc_traffic()
+    recur_cache = recurrence_cache_leg(args, torch, ops, sets, alpha, beta_stack, L, B * G * G * C, ms, nbytes["total"])
 
     # release every tensor and graph pool of the main measurement before the other legs
     outs = ref = None
@@ -803,7 +949,8 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        cpu = cpu_baseline(G, C, L, args.cpu_seconds)
+        cpu = cpu_baseline(B, G, C, L, args.cpu_seconds)
+        cpu["c_oracle"] = c_oracle_baseline(G, C, L, max(2.0, args.cpu_seconds / 4))
 
     line = {
         "metric": METRIC,
@@ -839,10 +986,12 @@ def main():
             "unit": "GB/s",
             "frac": round(mat_achieved / PEAK_HBM, 4),
             "traffic": traffic,
+            "traffic_source": traffic_source,
             "algorithmic_bytes_per_launch": nbytes["materialise"],
             "avg_launch_ms": round(mat_ms, 4),
         },
         "cpu_baseline": cpu,
+        "recurrence_mall": recur_cache,
         "model_fwd": model_fwd,
         "interface_train": train,
         "configs": configs,

@@ -27,6 +27,11 @@ def _per_channel(w: torch.Tensor, group_dim: int) -> torch.Tensor:
     return w if group_dim == 1 else w.repeat_interleave(group_dim, dim=0)
 
 
+def overridden(obj: nn.Module, name: str, base: type) -> bool:
+    """True when obj's hook `name` is not base's own: replaced on a subclass or assigned on the instance."""
+    return getattr(type(obj), name, None) is not getattr(base, name) or name in obj.__dict__
+
+
 class SharedLocalRead(nn.Module):
     """Depth-shared local read [B,Hh,Hh,C] -> [B,Gw*Gw,C] (local_thc.py:1166-1226)."""
 
@@ -75,7 +80,10 @@ class SharedLocalRead(nn.Module):
 
     def read_with_residual(self, x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
         """(x, read(x)) for the lazy forward, where x is read once here and materialised into at the end;
-        the backward returns dX = g_x + R^T(gZ0) in one pass (ops.read_with_residual)."""
+        the backward returns dX = g_x + R^T(gZ0) in one pass (ops.read_with_residual).  A replaced `read` or
+        `alpha` hook (subclass or instance) is honoured: then this is (x, self.read(x))."""
+        if overridden(self, "read", SharedLocalRead) or overridden(self, "alpha", SharedLocalRead):
+            return x, self.read(x)
         b, h, w, c = x.shape
         hh = self.high_grid
         if h != hh or w != hh or c != self.hidden_size:

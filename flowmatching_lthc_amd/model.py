@@ -29,7 +29,7 @@ import torch.nn.functional as F
 from torch.nn.attention import SDPBackend, sdpa_kernel
 
 from . import ops, ops_branch
-from .local_thc import LayerLocalWrite, SharedLocalRead
+from .local_thc import LayerLocalWrite, SharedLocalRead, overridden
 
 
 def modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
@@ -423,6 +423,10 @@ class SharedReadLocalTHCSharedAdaLNJiTBlock(nn.Module):
         gamma: this layer's gamma_from_alpha(shared_read.alpha(dz.dtype)) when the caller has computed it.
         split: return (z_next, z_next for the next block's branch, dz), whose backward also sums z_next's
         two gradients in that pass."""
+        if overridden(self, "lazy_workspace_update", SharedReadLocalTHCSharedAdaLNJiTBlock):
+            # a replaced reference hook (local_thc.py:1325) defines the step; gamma is its business
+            z_next = self.lazy_workspace_update(z, dz, shared_read)
+            return (z_next, z_next, dz) if split else (z_next, dz)
         if gamma is None:
             gamma = self.write.gamma_from_alpha(shared_read.alpha(dtype=dz.dtype))
         return ops.lazy_workspace_step(z, dz, gamma, split)
@@ -663,9 +667,13 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
         """Every block's gamma_from_alpha(shared_read.alpha(dz.dtype)) in one launch (ops.lazy_gamma_rounded: the
         same dtype sequence), or None where it does not apply (CPU, grouped write weights, another block type)."""
         writes = [blk.write for blk in self.blocks]
-        own_hooks = all(  # no block replaces the hook (subclass or instance override): it takes the gamma argument
-            type(blk).lazy_workspace_step is SharedReadLocalTHCSharedAdaLNJiTBlock.lazy_workspace_step
-            and "lazy_workspace_step" not in blk.__dict__
+        std = SharedReadLocalTHCSharedAdaLNJiTBlock
+        own_hooks = not overridden(self.shared_read, "alpha", SharedLocalRead) and all(
+            # no block replaces a hook the gammas come from (subclass or instance override)
+            not overridden(blk, "lazy_workspace_step", std)
+            and not overridden(blk, "lazy_workspace_update", std)
+            and not overridden(blk.write, "gamma_from_alpha", LayerLocalWrite)
+            and not overridden(blk.write, "beta", LayerLocalWrite)
             for blk in self.blocks
         )
         if not dz.is_cuda or not own_hooks or self.shared_read.group_dim != 1 or any(w.group_dim != 1 for w in writes):

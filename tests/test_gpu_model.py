@@ -173,3 +173,42 @@ def test_patch_embed_gather_cast_equals_autocast_cast():
         ref = F.linear(h, emb.proj2.weight.view(emb.proj2.out_channels, -1), emb.proj2.bias)
     assert got.dtype == ref.dtype == torch.bfloat16
     assert torch.equal(got, ref)
+
+
+def test_b4_configuration4_b64_matches_fp32_reference():
+    """Benchmark configuration 4 at its own size: LTHC-B/4 (random-init weights), B=64, images N(0,1)
+    [64,3,256,256], t ~ U(0,1), labels uniform in [0,1000), bf16 autocast, every fused HIP op in place
+    (interface kernels, fused attention, decoder head, block tails, one-launch weight casts).
+
+    The reference is an fp32 evaluation of the same weights through the fixture-pinned torch restatement (the
+    interface as the cell-reshape torch form, SDPA attention, the unfused decoder head; local_thc.py:1374-1394).
+    Bounds (errors in units of the reference output's largest magnitude, max|exact| ~ 3):
+      * max|ours - exact| <= 2e-2 * max|exact| (the stated bf16 bound, normalised to the output's scale);
+      * no further from exact than a bf16 autocast evaluation of the torch restatement (x1.5 slack);
+      * without autocast (fp32 throughout) the HIP path equals the fp32 restatement to 1e-4 relative.
+    """
+    print("case: lthc_b4_velocity B=64 bf16 autocast vs fp32 restatement", flush=True)
+    B = 64
+    ours = M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=11).to(DEV).eval()
+    ref = conv_interface(M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=11), "reshape").to(DEV).eval()
+    for blk in ref.blocks:
+        blk.branch.attn.fused_attention = False
+    ref.fused_decoder = False
+    gen = torch.Generator().manual_seed(12)
+    x = torch.randn(B, 3, 256, 256, generator=gen).to(DEV)
+    t = torch.rand(B, generator=gen).to(DEV)
+    y = torch.randint(0, 1000, (B,), generator=gen).to(DEV)
+    with torch.no_grad():
+        exact = ref(x, t, y, use_lazy=False).float()
+        ours32 = ours(x, t, y, use_lazy=True).float()
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            ours_bf = ours(x, t, y).float()
+            eager_bf = ref(x, t, y, use_lazy=True).float()
+    scale = exact.abs().max().item()
+    assert torch.isfinite(ours_bf).all() and scale > 0
+    err = (ours_bf - exact).abs().max().item() / scale
+    err_eager = (eager_bf - exact).abs().max().item() / scale
+    print(f"max|exact|={scale:.3f} bf16 err={err:.3e} eager bf16 err={err_eager:.3e} fp32 rel={rel(ours32, exact):.2e}")
+    assert err <= 2e-2, err
+    assert err <= max(1.5 * err_eager, 1e-3), (err, err_eager)
+    assert rel(ours32, exact) <= 1e-4

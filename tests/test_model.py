@@ -230,3 +230,69 @@ def test_legacy_hyper_connection_modules_on_cpu():
         LT.ChannelwiseLocalTokenHyperConnectionTriton(64, 16, 32, 32, use_softmax_write=False)
     with pytest.raises(ValueError, match="no CPU fallback"):
         m.read(torch.zeros(1, 64, 64, 32))
+
+
+def conv_read(model, x):
+    s, c = model.high_grid // model.workspace_grid, model.hidden_size
+    a = model.shared_read.alpha(dtype=x.dtype)
+    z = F.conv2d(x.permute(0, 3, 1, 2), a.reshape(c, 1, s, s), stride=s, groups=c)
+    return z.permute(0, 2, 3, 1).reshape(x.shape[0], -1, c)
+
+
+def conv_final(model, x0, dz_list):
+    s, c, g = model.high_grid // model.workspace_grid, model.hidden_size, model.workspace_grid
+    x = x0
+    for blk, dz in zip(model.blocks, dz_list, strict=True):
+        w = blk.write.beta(dtype=dz.dtype)
+        out = F.conv_transpose2d(dz.reshape(dz.shape[0], g, g, c).permute(0, 3, 1, 2), w.reshape(c, 1, s, s), stride=s, groups=c)
+        x = x + out.permute(0, 2, 3, 1)
+    return x
+
+
+def test_forward_lazy_calls_an_overridden_lazy_workspace_update():
+    """A reference-style instance override of lazy_workspace_update (local_thc.py:1325, called at :1384) and of
+    shared_read.read alone defines forward_lazy's recurrence and read: the fixture is reproduced through them, and
+    a changed update changes the output."""
+    fx = load_fixture()
+    calls = []
+    m = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG).eval()
+    m.load_state_dict(fx["state_dict"])
+    m.shared_read.read = lambda x: conv_read(m, x)
+    m.final_accumulate_reference = lambda x0, dzs: conv_final(m, x0, dzs)
+    for i, blk in enumerate(m.blocks):
+
+        def upd(z, dz, shared_read, b=blk, i=i, scale=1.0):
+            calls.append(i)
+            return z + scale * b.write.gamma_from_alpha(shared_read.alpha(dtype=dz.dtype))[None, None, :] * dz
+
+        blk.lazy_workspace_update = upd
+    with torch.no_grad():
+        out = m(fx["x"], fx["t"], fx["y"], use_lazy=True)
+    assert calls == list(range(CONFIG["depth"]))
+    assert rel(out, fx["out_lazy"]) <= 1e-5
+    for blk in m.blocks:  # a different recurrence must show in the output
+        f = blk.lazy_workspace_update
+        blk.lazy_workspace_update = lambda z, dz, sr, f=f: f(z, 2.0 * dz, sr)
+    with torch.no_grad():
+        assert rel(m(fx["x"], fx["t"], fx["y"], use_lazy=True), fx["out_lazy"]) > 1e-4
+
+
+def test_overridden_gamma_or_alpha_hooks_disable_the_one_launch_gammas():
+    """_all_gammas (one launch for every block's gamma) stands aside whenever a hook it would bypass is replaced."""
+    m = M.SharedReadLocalTHCSharedAdaLNJiT(**CONFIG)
+    from flowmatching_lthc_amd.local_thc import LayerLocalWrite, SharedLocalRead, overridden
+
+    std = M.SharedReadLocalTHCSharedAdaLNJiTBlock
+    blk = m.blocks[0]
+    assert not overridden(blk, "lazy_workspace_update", std)
+    assert not overridden(blk.write, "gamma_from_alpha", LayerLocalWrite)
+    blk.write.gamma_from_alpha = lambda a: a.sum(-1)
+    assert overridden(blk.write, "gamma_from_alpha", LayerLocalWrite)
+
+    class Sub(SharedLocalRead):
+        def alpha(self, dtype=None):
+            return super().alpha(dtype)
+
+    sr = Sub(8, 2, CONFIG["hidden_size"], CONFIG["hidden_size"])
+    assert overridden(sr, "alpha", SharedLocalRead)
+    assert not overridden(m.shared_read, "alpha", SharedLocalRead)

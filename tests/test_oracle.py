@@ -359,3 +359,29 @@ def test_mutation_wrong_sign_in_backward_is_caught():
     got = O.interface_bwd_np(cs["x0"], cs["alpha"], cs["dzs"], cs["betas"], cs["grad_xl"], [-gz for gz in cs["grad_zs"]], cs["g"])
     assert not np.allclose(got["dz"][0], ref["dz"][0])
     assert not np.allclose(got["alpha"], ref["alpha"])
+
+
+def test_torch_cpu_sequence_matches_numpy_oracle():
+    """oracle/torch_cpu.py (the reference's eager op sequence, timed as the CPU baseline) equals the numpy oracle's
+    read, gamma, recurrence and materialisation, which the depthwise-convolution and brute-force checks above pin."""
+    import torch
+
+    from oracle import torch_cpu as TC
+
+    B, G, C, L = 2, 4, 12, 3
+    d = O.make_inputs(B, G, C, L, seed=5)
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).double()  # noqa: E731
+    x0, alpha = t(d["x0"]), t(d["alpha"])
+    betas, dzs = [t(b) for b in d["beta"]], [t(z) for z in d["dz"]]
+    np.testing.assert_allclose(TC.read(x0, alpha, G).numpy(), O.read_np(d["x0"], d["alpha"], G), rtol=1e-12, atol=1e-12)
+    for l in range(L):
+        np.testing.assert_allclose(TC.gamma(alpha, betas[l]).numpy(), O.gamma_np(d["alpha"], d["beta"][l]), rtol=1e-12)
+    zl, xl = TC.step(x0, alpha, betas, dzs, G)
+    z_ref = O.read_np(d["x0"], d["alpha"], G)
+    for l in range(L):
+        z_ref = O.lazy_update_np(z_ref, d["dz"][l], O.gamma_np(d["alpha"], d["beta"][l]))
+    np.testing.assert_allclose(zl.numpy(), z_ref, rtol=1e-12, atol=1e-12)
+    xl_ref = O.final_accumulate_np(d["x0"], list(d["dz"]), list(d["beta"]))
+    np.testing.assert_allclose(xl.numpy(), xl_ref, rtol=1e-12, atol=1e-12)
+    # the lazy identity holds through this sequence too: R(X_L) == Z_L
+    np.testing.assert_allclose(TC.read(xl, alpha, G).numpy(), zl.numpy(), rtol=1e-10, atol=1e-10)
