@@ -109,5 +109,5 @@ def test_recurrence_rounding_against_eager(dtype):
     e_eager = (eager.double() - exact).abs()
     assert (e_ours <= u * (1 + 2.0**-12) * exact.abs() + tiny).all()  # fp32 fma, then one rounding
     assert (e_eager <= u * prod + u * eager.double().abs() + tiny).all()
-    assert (ours != eager).double().mean().item() <= 0.1
+    assert (ours != eager).double().mean().item() <= 0.25  # about 10 % here, where gamma dz is ~0.15 z
     assert e_ours.mean().item() <= e_eager.mean().item()
