@@ -223,6 +223,17 @@ LTHC_DEV float round_w(float v) {
   else return static_cast<float>(static_cast<_Float16>(v));
 }
 
+// fp16 outputs of an fma chain are rounded once from the fp32 result: the empty asm keeps the compiler from folding
+// the last fma and the narrowing into a mixed-precision fma (one rounding of the exact value) for some lanes or
+// kernels and not others, so every kernel producing the same quantity gives the same bits.
+template <int DT, int N>
+LTHC_DEV void hold_f32(float (&v)[N]) {
+  if constexpr (DT == LTHC_F16) {
+#pragma unroll
+    for (int i = 0; i < N; ++i) asm volatile("" : "+v"(v[i]));
+  }
+}
+
 LTHC_DEV void store_w(void* __restrict__ p, int dt, int64_t i, float v) {
   if (dt == LTHC_F32) {
     static_cast<float*>(p)[i] = v;
@@ -408,7 +419,10 @@ __global__ __launch_bounds__(kBlock) void cell_mat_kernel(const void* __restrict
         for (int v = 0; v < CPT; ++v) acc[k][v] = fmaf(bw[l][v][k], d[v], acc[k][v]);
     }
 #pragma unroll
-    for (int k = 0; k < TPT; ++k) store_at<DT, CPT, true>(out, xo + (k / kS) * row_b + (k % kS) * tap_b, acc[k]);
+    for (int k = 0; k < TPT; ++k) {
+      hold_f32<DT>(acc[k]);
+      store_at<DT, CPT, true>(out, xo + (k / kS) * row_b + (k % kS) * tap_b, acc[k]);
+    }
   }
 }
 
@@ -496,7 +510,10 @@ __global__ __launch_bounds__(kBlock) void materialise_kernel(const void* __restr
         for (int v = 0; v < CPT; ++v) acc[j][v] = fmaf(bw[l][v][j], d[v], acc[j][v]);
     }
 #pragma unroll
-    for (int j = 0; j < TPT; ++j) store_at<DT, CPT, NT>(out, xo + j * tap_b, acc[j]);
+    for (int j = 0; j < TPT; ++j) {
+      hold_f32<DT>(acc[j]);
+      store_at<DT, CPT, NT>(out, xo + j * tap_b, acc[j]);
+    }
   }
 }
 
@@ -558,8 +575,10 @@ __global__ __launch_bounds__(kBlock) void read_multi_kernel(const void* __restri
         for (int v = 0; v < 4; ++v) acc[i][v] = fmaf(gv[v], wr[i][v][k], acc[i][v]);
     }
 #pragma unroll
-    for (int i = 0; i < LC; ++i)
+    for (int i = 0; i < LC; ++i) {
+      hold_f32<DT>(acc[i]);
       if (i < nl) store_at<DT, 4>(const_cast<void*>(out.p[l0 + i]), zo, acc[i]);
+    }
   }
 }
 
@@ -701,8 +720,10 @@ __global__ __launch_bounds__(kBlock) void cell_read_multi_kernel(const void* __r
         for (int v = 0; v < CPT; ++v) acc[i][v] = fmaf(gv[v], wr[i][v][k], acc[i][v]);
     }
 #pragma unroll
-    for (int i = 0; i < LPG; ++i)
+    for (int i = 0; i < LPG; ++i) {
+      hold_f32<DT>(acc[i]);
       if (EXACT || l0 + i < L) store_at<DT, CPT, true>(const_cast<void*>(out.p[l0 + i]), zo, acc[i]);
+    }
   }
 }
 
@@ -1969,6 +1990,8 @@ int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, cons
 #include "decoder.inc"
 // One-launch dtype conversion of many weights (autocast's per-forward casts).
 #include "cast_many.inc"
+// LDS-staged backward tiles: the materialise backward and the single-pass interface backward.
+#include "bwd_tile.inc"
 // Fused materialise backward (gdZ and gbeta from one pass over G).
 #include "materialise_bwd.inc"
 // Whole-interface entry points: recurrence prefix, read backward, interface forward / backward.
