@@ -33,6 +33,8 @@ EXPORTS = (
     "lthc_weight_grad",
     "lthc_materialise_bwd_workspace_bytes",
     "lthc_materialise_bwd",
+    "lthc_noalloc_scratch_bytes",
+    "lthc_materialise_bwd_noalloc",
     "lthc_gamma",
     "lthc_gamma_rounded",
     "lthc_gamma_rounded_bwd",
@@ -92,6 +94,7 @@ def load() -> ctypes.CDLL:
         "lthc_materialise_fwd": [vp, pp, ci, pp, ci, vp, i64, i64, i64, i64, ci, vp],
         "lthc_weight_grad": [vp, pp, ci, vp, i64, i64, i64, i64, ci, vp, sz, vp],
         "lthc_materialise_bwd": [vp, ci, pp, pp, ci, pp, vp, i64, i64, i64, i64, ci, vp, sz, vp],
+        "lthc_materialise_bwd_noalloc": [vp, ci, pp, pp, ci, pp, vp, i64, i64, i64, i64, ci, vp],
         "lthc_gamma": [vp, pp, ci, vp, ci, i64, i64, ci, vp],
         "lthc_gamma_rounded": [vp, ci, pp, ci, vp, ci, i64, i64, ci, vp],
         "lthc_gamma_rounded_bwd": [vp, vp, ci, pp, ci, vp, pp, ci, i64, i64, ci, vp],
@@ -133,6 +136,8 @@ def load() -> ctypes.CDLL:
     lib.lthc_weight_grad_workspace_bytes.restype = sz
     lib.lthc_materialise_bwd_workspace_bytes.argtypes = [i64, i64, i64, i64, ci]
     lib.lthc_materialise_bwd_workspace_bytes.restype = sz
+    lib.lthc_noalloc_scratch_bytes.argtypes = []
+    lib.lthc_noalloc_scratch_bytes.restype = sz
     lib.lthc_read_bwd_workspace_bytes.argtypes = [i64, i64, i64, i64]
     lib.lthc_read_bwd_workspace_bytes.restype = sz
     lib.lthc_interface_workspace_bytes.argtypes = [i64, i64, i64, i64, ci]

@@ -1996,3 +1996,5 @@ int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, cons
 #include "materialise_bwd.inc"
 // Whole-interface entry points: recurrence prefix, read backward, interface forward / backward.
 #include "interface.inc"
+// The materialise backward without a caller workspace (a file-scope scratch array per GPU).
+#include "noalloc.inc"

@@ -146,6 +146,22 @@ int lthc_materialise_bwd(const void* g, int x_dtype, const void* const* dz, cons
                          void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * MATERIALISE BACKWARD WITHOUT A WORKSPACE: lthc_materialise_bwd with the fp32
+ * partial sums in a scratch array the library holds on every GPU it runs on
+ * (lthc_noalloc_scratch_bytes() = 64 MiB, kept until the process ends).  No
+ * counterpart in the reference: it is for callers that cannot allocate (code
+ * under HIP graph capture, serving loops, harnesses that forbid hipMalloc).  It
+ * calls no allocator.  Shapes whose partials need more than the scratch array
+ * (lthc_materialise_bwd_workspace_bytes() > 64 MiB) return LTHC_ERR_UNSUPPORTED.
+ * All calls on one GPU share the array, which keeps the last call's contents:
+ * calls that overlap on one GPU race; the caller serialises them.
+ */
+size_t lthc_noalloc_scratch_bytes(void);
+int lthc_materialise_bwd_noalloc(const void* g, int x_dtype, const void* const* dz, const void* const* beta,
+                                 int w_dtype, void* const* gdz, float* gbeta, int64_t B, int64_t G, int64_t s,
+                                 int64_t C, int L, void* stream);
+
+/*
  * GAMMA   gamma_l[c] = sum_k alpha[c,k] * beta_l[c,k]   (written in out_dtype)
  * Replaces LayerLocalWrite.gamma_from_alpha (local_thc.py:1278-1283), computed
  * here in fp32 from the given weights.  `beta` is a host array of L device
