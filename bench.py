@@ -60,12 +60,13 @@ def parse_args():
         "--profile",
         choices=[
             "materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model", "train", "triangular",
-            "interface_c",
+            "interface_c", "mat_bwd", "interface_bwd",
         ],  # fmt: skip
         help="run only this kernel --steps times at the configured shape (for rocprofv3), plus one plain copy "
         "of X0 (a copy kernel of known size that calibrates the FETCH_SIZE / WRITE_SIZE counters); 'model' runs "
         "only the LTHC-B/4 forward leg (without the eager-interface comparison), 'train' only the interface fwd+bwd leg, 'triangular' only the non-shared "
-        "interface forward leg, 'interface_c' only the whole-interface C calls at the training batch",
+        "interface forward leg, 'interface_c' only the whole-interface C calls at the training batch; 'mat_bwd' is "
+        "lthc_materialise_bwd and 'interface_bwd' lthc_interface_bwd (every workspace gradient given) at --batch",
     )
     return p.parse_args()
 
@@ -427,8 +428,10 @@ def interface_c_level(args, torch, dev, B, G, C, L):
     """The whole-interface C entry points with every dZ_l given (lthc_interface_fwd, lthc_interface_bwd): one call
     each, no autograd, events around `steps` calls over two input sets.  Not the metric's step (the model's lazy
     forward runs a branch between the recurrence steps); reported beside it.  Bytes: forward e(3T + (3L + 2)W)
-    (read, prefix recurrence e(W + 2LW), materialise); backward e(4T + 6LW + 3W): materialise backward e(T + 2LW),
-    the one-pass recurrence backward e(4LW + W), the read backward's dX0 e(2T + W) and dalpha e(T + W)."""
+    (read, prefix recurrence e(W + 2LW), materialise).  Backward: the single-pass compulsory bytes e(3T + 3LW) (read
+    G_L, X0, the H and dZ stacks; write dX0 and the dZ-gradient stack), against which the rate is reported; the
+    implementation moves e(3T + 3LW + 2W): the tile kernel e(2T + 3LW + W) (it also writes S_0) and dalpha's pass
+    over X0 and S_0 e(T + W)."""
     from flowmatching_lthc_amd import _abi
 
     lib = _abi.load()
@@ -488,7 +491,7 @@ def interface_c_level(args, torch, dev, B, G, C, L):
     fwd_ms, bwd_ms = timed(fwd), timed(bwd)
     T, W = B * H * H * C, B * G * G * C
     fb = 2 * (3 * T + (3 * L + 2) * W)
-    bb = 2 * (4 * T + 6 * L * W + 3 * W)
+    bb = 2 * (3 * T + 3 * L * W)
     out = {
         "workload": f"whole-interface C calls, every dZ_l given (B={B}, {H}x{H}/{G}x{G}, C={C}, L={L}, bf16, fp32 weights)",
         "timing": "events around consecutive calls, eager (several launches per call)",
@@ -497,7 +500,9 @@ def interface_c_level(args, torch, dev, B, G, C, L):
         "fwd_GBps": round(fb / (fwd_ms * 1e-3) / 1e9, 1),
         "bwd_ms": round(bwd_ms, 4),
         "bwd_bytes": bb,
+        "bwd_byte_definition": "single-pass compulsory e(3T + 3LW); the implementation moves e(3T + 3LW + 2W)",
         "bwd_GBps": round(bb / (bwd_ms * 1e-3) / 1e9, 1),
+        "bwd_pct_of_peak_hbm": round(100.0 * bb / (bwd_ms * 1e-3) / PEAK_HBM, 2),
     }
     del sets, zs, xl, ws, gx, gzs, dx0, ddz
     torch.cuda.synchronize()
@@ -700,9 +705,9 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
     T = B * H * H * C
     W = B * G * G * C
     fused_bwd = 2 * (3 * T + 3 * L * W)
-    # per-op compulsory bytes: materialise backward e(T + 2LW) (gdZ and gbeta from one read of G_L), recurrence
-    # backward e(6LW) (per layer g, dz, the branch gradient and the materialisation's gradient in, two out), read
-    # backward e(3T + W) (G_L, gZ0 and X0 in, dX0 out)
+    # per-op compulsory bytes: materialise backward e(T + 2LW) (gdZ and gbeta from one read of G_L: the tile kernel
+    # bwd_tile_kernel), recurrence backward e(6LW) (per layer g, dz, the branch gradient and the materialisation's
+    # gradient in, two out), read backward e(3T + W) (G_L, gZ0 and X0 in, dX0 out)
     per_op_bwd = 2 * (4 * T + 8 * L * W + W)
     fwd_ms, step_ms = (graph_fwd, graph_step) if graph_error is None else (eager_fwd, eager_step)
     bwd_ms = step_ms - fwd_ms
@@ -724,8 +729,8 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
         "bwd_per_op_GBps": round(per_op_bwd / (bwd_ms * 1e-3) / 1e9, 1),
         "byte_definition": "bwd_single_pass_bytes = e*(3T + 3LW): the compulsory bytes of a fused single-pass backward "
         "(read G_L, X0, H stack, dZ stack; write dX0, dZ-grad stack); bwd_per_op_bytes = e*(4T + 8LW + W): each "
-        "backward op's compulsory bytes (materialise e(T+2LW), L recurrence steps e(6LW), read e(3T+W)); the "
-        "launched ops move more (G_L is read twice by the materialise backward)",
+        "backward op's compulsory bytes (materialise e(T+2LW), L recurrence steps e(6LW), read e(3T+W)); autograd "
+        "runs these ops, so G_L is read twice (materialise backward, read backward)",
     }
 
 
@@ -780,6 +785,48 @@ def profile(args, ops, inputs, alpha, beta_stack, betas):
     x0, dzs = inputs
     z = ops.local_write_traceable(x0, alpha)
     gam = ops.lazy_gamma_stack(alpha, beta_stack)
+    if args.profile in ("mat_bwd", "interface_bwd"):
+        import ctypes
+
+        from flowmatching_lthc_amd import _abi
+
+        lib = _abi.load()
+        B, H, C = x0.shape[0], x0.shape[1], x0.shape[3]
+        G, L = H // 4, len(dzs)
+        sid = torch.cuda.current_stream().cuda_stream
+        gdz = [torch.empty_like(d) for d in dzs]
+        gb = torch.empty((L, C, 16), device=x0.device)
+        if args.profile == "mat_bwd":  # G_L = x0's values (the data do not change the traffic)
+            ws = torch.empty((int(lib.lthc_materialise_bwd_workspace_bytes(B, G, 4, C, L)),), device=x0.device,
+                             dtype=torch.uint8)  # fmt: skip
+
+            def run():
+                _abi.check(lib.lthc_materialise_bwd(
+                    x0.data_ptr(), _abi.code(x0), _abi.ptr_array(dzs), _abi.ptr_array(betas), _abi.code(alpha),
+                    _abi.ptr_array(gdz), gb.data_ptr(), B, G, 4, C, L, ws.data_ptr(), ws.numel(), sid,
+                ), "lthc_materialise_bwd")  # fmt: skip
+        else:  # G_L = x0; H_l tensors of their own (aliasing dZ_l would serve them from cache)
+            ws = torch.empty((int(lib.lthc_interface_workspace_bytes(B, G, 4, C, L)),), device=x0.device,
+                             dtype=torch.uint8)  # fmt: skip
+            dx0 = torch.empty_like(x0)
+            da = torch.empty((C, 16), device=x0.device)
+            hs = [d * 0.5 for d in dzs]
+            gz = (ctypes.c_void_p * L)(*[h.data_ptr() for h in hs])
+
+            def run():
+                _abi.check(lib.lthc_interface_bwd(
+                    x0.data_ptr(), gz, _abi.code(x0), x0.data_ptr(), _abi.ptr_array(dzs), alpha.data_ptr(),
+                    _abi.ptr_array(betas), _abi.code(alpha), dx0.data_ptr(), _abi.ptr_array(gdz), da.data_ptr(),
+                    gb.data_ptr(), B, G, 4, C, L, ws.data_ptr(), ws.numel(), sid,
+                ), "lthc_interface_bwd")  # fmt: skip
+        for _ in range(args.warmup + args.steps):
+            run()
+        torch.cuda.synchronize()
+        y = torch.empty_like(x0)
+        y.copy_(x0)
+        torch.cuda.synchronize()
+        print(f"profiled {args.profile} x{args.warmup + args.steps}; calibration copy of {x0.numel() * x0.element_size()} bytes")
+        return
     run = {
         "materialise": lambda: ops.final_accumulate_b4_12_traceable(x0, *dzs, *betas),
         "read": lambda: ops.local_write_traceable(x0, alpha),
