@@ -136,9 +136,11 @@ int lthc_weight_grad(const void* high, const void* const* low, int x_dtype, floa
  * (local_thc_triton_kernels.py:512-680, 1800-1894): the same two results as
  * lthc_read_multi_fwd(G, beta) and lthc_weight_grad(G, dz), but G (the
  * largest tensor) is read once instead of twice.  gdz is bitwise equal to
- * lthc_read_multi_fwd's.  One kernel when L <= 24, C % 64 == 0 and G is
- * below 4 GiB; otherwise the two separate passes.  `dz`, `beta`, `gdz`
- * are host arrays of L device pointers; the workspace holds the fp32 partials.
+ * lthc_read_multi_fwd's.  One LDS-staged tile kernel for 16-bit activations
+ * with L <= 12, C % 64 == 0, G % 8 == 0 and 16-byte aligned dz; otherwise one
+ * register kernel when L <= 24, C % 64 == 0 and G is below 4 GiB; otherwise
+ * the two separate passes.  `dz`, `beta`, `gdz` are host arrays of L device
+ * pointers; the workspace holds the fp32 partials.
  */
 size_t lthc_materialise_bwd_workspace_bytes(int64_t B, int64_t G, int64_t s, int64_t C, int L);
 int lthc_materialise_bwd(const void* g, int x_dtype, const void* const* dz, const void* const* beta, int w_dtype,
@@ -438,11 +440,16 @@ int lthc_read_bwd(const void* gz, const void* x, int x_dtype, const void* alpha,
  *             dbeta[l] = sum gx dz_l + (sum S_{l+1} dz_l) alpha;
  *             dalpha = sum x0 S_0 + sum_l (sum S_{l+1} dz_l) beta_l
  *             (dalpha [C,16], dbeta [L,C,16] fp32; fixed-order reductions).
- * Compositions of the per-op entry points (read, gamma, recurrence prefix,
- * materialise; materialise backward, read backward); up to depth 24 the
- * backward's recurrence steps run in one pass over H, dZ and gdZ, giving the
- * per-step entry points' values bit for bit (one lthc_recur_bwd or
- * lthc_recur_bwd_sum per step above that depth).
+ * The forward composes the per-op entry points (read, gamma, recurrence
+ * prefix, materialise).  The backward is one pass over gx and the dz and gz
+ * stacks for 16-bit activations with L <= 12, C % 64 == 0, G % 8 == 0 and
+ * 16-byte aligned gx, dx0 and alpha (one tile kernel writes ddz, dx0 and S_0
+ * and the partial sums of dbeta's and the gamma terms; then dalpha's pass over
+ * x0 and S_0), and otherwise a composition (materialise backward; the
+ * recurrence steps in one pass over H, dZ and gdZ up to depth 24, one
+ * lthc_recur_bwd or lthc_recur_bwd_sum per step above; read backward).  Both
+ * give the per-step entry points' ddz and dx0 bit for bit (local_thc_triton_kernels.py:512-680,
+ * 1800-1919 and the eager autograd of local_thc.py:1211-1223, 1325-1328).
  * One caller workspace of lthc_interface_workspace_bytes() serves both.
  */
 size_t lthc_interface_workspace_bytes(int64_t B, int64_t G, int64_t s, int64_t C, int L);
