@@ -51,6 +51,8 @@ EXPORTS = (
     "lthc_qk_norm_rope",
     "lthc_qk_norm_rope_attention",
     "lthc_decoder_fwd",
+    "lthc_materialise_decoder_workspace_bytes",
+    "lthc_materialise_decoder_fwd",
     "lthc_cast_many",
     "lthc_swiglu",
     "lthc_gate_add_norm_modulate_fwd",
@@ -111,6 +113,10 @@ def load() -> ctypes.CDLL:
         "lthc_decoder_fwd": [
             vp, ci, vp, ci, vp, vp, i64, vp, ci, vp, ci, vp, i64, i64, i64, i64, i64, i64, ctypes.c_float, vp,
         ],  # fmt: skip
+        "lthc_materialise_decoder_fwd": [
+            vp, ci, pp, pp, ci, vp, ci, vp, vp, i64, vp, ci, vp, ci, vp, i64, i64, i64, i64, ci, i64, i64,
+            ctypes.c_float, vp, sz, vp,
+        ],  # fmt: skip
         "lthc_cast_many": [vp, vp, i64, vp, ci, vp],
         "lthc_swiglu": [vp, ci, vp, i64, i64, vp],
         "lthc_gate_add_norm_modulate_fwd": [
@@ -138,6 +144,8 @@ def load() -> ctypes.CDLL:
     lib.lthc_materialise_bwd_workspace_bytes.restype = sz
     lib.lthc_noalloc_scratch_bytes.argtypes = []
     lib.lthc_noalloc_scratch_bytes.restype = sz
+    lib.lthc_materialise_decoder_workspace_bytes.argtypes = [i64, i64, i64, i64]
+    lib.lthc_materialise_decoder_workspace_bytes.restype = sz
     lib.lthc_read_bwd_workspace_bytes.argtypes = [i64, i64, i64, i64]
     lib.lthc_read_bwd_workspace_bytes.restype = sz
     lib.lthc_interface_workspace_bytes.argtypes = [i64, i64, i64, i64, ci]
@@ -192,6 +200,10 @@ def weight_grad_workspace_bytes(B: int, G: int, S: int, C: int, L: int) -> int:
 
 def materialise_bwd_workspace_bytes(B: int, G: int, S: int, C: int, L: int) -> int:
     return int(load().lthc_materialise_bwd_workspace_bytes(B, G, S, C, L))
+
+
+def materialise_decoder_workspace_bytes(B: int, G: int, S: int, C: int) -> int:
+    return int(load().lthc_materialise_decoder_workspace_bytes(B, G, S, C))
 
 
 def recur_bwd_workspace_bytes(rows: int, C: int) -> int:

@@ -1998,3 +1998,5 @@ int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, cons
 #include "interface.inc"
 // The materialise backward without a caller workspace (a file-scope scratch array per GPU).
 #include "noalloc.inc"
+// The materialisation with the decoder front in its epilogue (no-grad forwards).
+#include "mat_decoder.inc"

@@ -526,6 +526,9 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
         # inference: each block's last gated residual, its recurrence step and the next block's first pre-norm in
         # one HIP pass (jit_thc::block_tail)
         self.fused_block_tail = True
+        # inference: the final materialisation with the decoder's norm, modulation and linear layer in its
+        # epilogue, X_L never written (jit_thc::final_accumulate_decoder_head)
+        self.fused_materialise_decoder = True
 
     # -- initialisation (local_thc.py:944-970, :1004-1007) ------------------------------------------
     def initialize_weights(self) -> None:
@@ -593,6 +596,38 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
             return ops.decoder_head(x, fl.norm_final.weight, shift, scale, lw, lb, fl.norm_final.eps, hh, self.patch_size)
         return self.unpatchify(fl(x, t2))
 
+    def _materialise_decode(self, x0: torch.Tensor, dz_list: list[torch.Tensor], t2: torch.Tensor) -> torch.Tensor:
+        """decode(X_L) for X_L = x0 + sum_l P_l(dZ_l).  Under no-grad on the GPU, with the standard final layer and
+        materialisation hooks, one pass forms X_L per token and feeds it to the decoder's norm, modulation and linear
+        layer without writing it (jit_thc::final_accumulate_decoder_head); otherwise X_L, then the decoder."""
+        fl = self.final_layer
+        if (
+            self.fused_materialise_decoder
+            and self.fused_decoder
+            and not torch.is_grad_enabled()
+            and type(fl) is FinalLayerSharedAdaLN
+            and "forward" not in fl.__dict__
+            and isinstance(fl.norm_final, RMSNorm)
+            and fl.linear.bias is not None
+            and "final_accumulate_reference" not in self.__dict__
+            and type(self).final_accumulate_reference
+            in (
+                SharedReadLocalTHCSharedAdaLNJiT.final_accumulate_reference,
+                SharedReadFusedFinal12LocalTHCSharedAdaLNJiT.final_accumulate_reference,
+            )
+            and len(dz_list) == len(self.blocks)
+            and t2.dtype == x0.dtype
+            and all(dz.dtype == x0.dtype and dz.is_cuda for dz in dz_list)
+            and ops.materialise_decoder_supported(x0, dz_list, fl.linear.weight, self.patch_size)
+        ):
+            betas = [blk.write.channel_beta(dtype=torch.float32) for blk in self.blocks]
+            shift, scale = t2.chunk(2, dim=1)
+            lw, lb = fl.linear.__dict__.get("_cast") or (fl.linear.weight, fl.linear.bias)
+            return ops.final_accumulate_decoder_head(
+                x0, list(dz_list), betas, fl.norm_final.weight, shift, scale, lw, lb, fl.norm_final.eps, self.patch_size
+            )
+        return self._decode(self.final_accumulate_reference(x0, dz_list), t2)
+
     def forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         t6, t2 = self._conditioning(t, y)
         # local_thc.py:1376-1385 (read once, one branch + recurrence per block, one materialisation).  The read
@@ -602,7 +637,7 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
         if self._tail_fusable(z):
             dz_list = self._blocks_fused_tail(z, t6)
             if dz_list is not None:
-                return self._decode(self.final_accumulate_reference(x0, dz_list), t2)
+                return self._materialise_decode(x0, dz_list, t2)
         zb = z  # the next branch's input: z itself, or the step's branch output (same values)
         dz_list, gammas = [], None
         for i, block in enumerate(self.blocks):
@@ -615,7 +650,7 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
             else:
                 z, zb, dz = block.lazy_workspace_step(z, dz, self.shared_read, gammas[i], split=True)
             dz_list.append(dz)
-        return self._decode(self.final_accumulate_reference(x0, dz_list), t2)
+        return self._materialise_decode(x0, dz_list, t2)
 
     def _tail_fusable(self, z: torch.Tensor) -> bool:
         """Inference on the GPU with the standard blocks, hooks, branch and ungrouped weights: jit_thc::block_tail

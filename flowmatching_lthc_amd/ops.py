@@ -1259,6 +1259,76 @@ def decoder_head(
     return img
 
 
+def materialise_decoder_supported(x0: Tensor, dzs: Sequence[Tensor], lin_weight: Tensor, patch: int) -> bool:
+    """Whether jit_thc::final_accumulate_decoder_head takes these operands: bf16 / fp16 x0 [B, 4G, 4G, C] with
+    G % 16 == 0, C % 256 == 0, 1..12 layers, 48 outputs per token, below 4 GiB."""
+    if not (x0.is_cuda and x0.dim() == 4 and x0.dtype in (torch.bfloat16, torch.float16)):
+        return False
+    b, h, w, c = x0.shape
+    return (
+        h == w
+        and h % (4 * 16) == 0
+        and c % 256 == 0
+        and 1 <= len(dzs) <= 12
+        and patch > 0
+        and DECODER_OUTPUTS % (patch * patch) == 0
+        and tuple(lin_weight.shape) == (DECODER_OUTPUTS, c)
+        and x0.numel() * 2 < 2**32
+    )
+
+
+@torch.library.custom_op("jit_thc::final_accumulate_decoder_head", mutates_args=())
+def final_accumulate_decoder_head(
+    x0: Tensor, dzs: list[Tensor], betas: list[Tensor], norm_weight: Tensor, shift: Tensor, scale: Tensor,
+    lin_weight: Tensor, lin_bias: Tensor, eps: float, patch: int,
+) -> Tensor:
+    """The model's last two steps for no-grad forwards: X_L = x0 + sum_l P_l(dzs[l]) (local_thc.py:1368-1372)
+    and unpatchify(Linear(modulate(RMSNorm(X_L), shift, scale))) (:865-873, :972-980), with X_L formed per token in
+    registers and never written (lthc_materialise_decoder_fwd).  X_L is rounded to x0.dtype as the materialisation
+    rounds it; the norm, modulation and linear layer are computed as inv * (x . M_b) + Q_b in fp32 without the
+    eager sequence's intermediate roundings.  Returns the image [B, CO, 4G*P, 4G*P] in x0.dtype.  Inference only:
+    no autograd formula."""
+    _on_gpu(x0, *dzs, *betas, norm_weight, shift, scale, lin_weight, lin_bias)
+    _check_list(x0, dzs, betas)
+    if not materialise_decoder_supported(x0, dzs, lin_weight, patch):
+        raise ValueError(
+            f"x0 must be bf16 or fp16 [B, 4G, 4G, C] with G % 16 == 0, C % 256 == 0, 1..12 layers and lin_weight "
+            f"[{DECODER_OUTPUTS}, C]; got {tuple(x0.shape)} {x0.dtype}, {len(dzs)} layers, {tuple(lin_weight.shape)}"
+        )
+    b, h, _, c = x0.shape
+    g = h // S
+    co = DECODER_OUTPUTS // (patch * patch)
+    for name, v in (("shift", shift), ("scale", scale)):
+        if tuple(v.shape) != (b, c) or v.dtype != x0.dtype:
+            raise ValueError(f"{name} must be [{b}, {c}] {x0.dtype}, got {tuple(v.shape)} {v.dtype}")
+    if tuple(norm_weight.shape) != (c,) or tuple(lin_bias.shape) != (DECODER_OUTPUTS,):
+        raise ValueError(f"norm_weight [{c}] and lin_bias [{DECODER_OUTPUTS}] expected")
+    x0 = _prep(x0)
+    dzs = _same_dtype(x0, [_prep(d) for d in dzs])
+    betas = [_prep_w(bt, torch.float32).float() for bt in betas]
+    (shift, scale), ld = _mod_rows(shift, scale, elems=1)
+    nw = _norm_weight(norm_weight)
+    lw = (lin_weight if lin_weight.dtype in (torch.float32, x0.dtype) else lin_weight.float()).contiguous()
+    lb = (lin_bias if lin_bias.dtype in (torch.float32, x0.dtype) else lin_bias.float()).contiguous()
+    img = torch.empty((b, co, h * patch, h * patch), device=x0.device, dtype=x0.dtype)
+    ws = torch.empty((max(_abi.materialise_decoder_workspace_bytes(b, g, S, c), 16),), device=x0.device, dtype=torch.uint8)
+    with _on_device(x0):
+        rc = _abi.load().lthc_materialise_decoder_fwd(
+            x0.data_ptr(), _abi.code(x0), _abi.ptr_array(dzs), _abi.ptr_array(betas), _abi.code(betas[0]),
+            nw.data_ptr(), _abi.code(nw), shift.data_ptr(), scale.data_ptr(), ld, lw.data_ptr(), _abi.code(lw),
+            lb.data_ptr(), _abi.code(lb), img.data_ptr(), b, g, S, c, len(dzs), patch, co, eps, ws.data_ptr(),
+            ws.numel(), _abi.stream_of(x0),
+        )  # fmt: skip
+    _abi.check(rc, "lthc_materialise_decoder_fwd")
+    return img
+
+
+@final_accumulate_decoder_head.register_fake
+def _(x0, dzs, betas, norm_weight, shift, scale, lin_weight, lin_bias, eps, patch):
+    b, h, _, _ = x0.shape
+    return x0.new_empty((b, DECODER_OUTPUTS // (patch * patch), h * patch, h * patch))
+
+
 @decoder_head.register_fake
 def _(x, norm_weight, shift, scale, lin_weight, lin_bias, eps, h, patch):
     b, t, _ = x.shape

@@ -347,6 +347,35 @@ int lthc_decoder_fwd(const void* x, int x_dtype, const void* norm_weight, int nw
                      float eps, void* stream);
 
 /*
+ * MATERIALISATION WITH THE DECODER FRONT IN ITS EPILOGUE (no-grad forwards;
+ * no reference op: the final materialisation, local_thc.py:1368-1372, followed
+ * by FinalLayerSharedAdaLN.forward and unpatchify, :865-873 and :972-980).
+ * X_L = x0 + sum_l P_l(dz[l]) is formed per token in registers, rounded to
+ * x_dtype as the materialisation rounds it, and never written; for each token
+ *   o[j] = r(inv * sum_c x[c] M_b[j,c] + Q_b[j]),  inv = 1/sqrt(mean_c x[c]^2 + eps)
+ *   M_b[j,c] = r(norm_weight[c] * r(1 + scale[b,c]) * r(W[j,c])),
+ *   Q_b[j] = sum_c shift[b,c] r(W[j,c]) + r(bias[j])  (fp32),
+ * r() the rounding to x_dtype; img[b, ci, hp*P + p1, wp*P + p2] =
+ * o[(hp, wp), (p1*P + p2)*CO + ci] in x_dtype, img [B, CO, 4G*P, 4G*P].
+ * This is modulate(RMSNorm(x)) @ W^T + bias without the eager sequence's
+ * roundings of the normalised and modulated rows (compare with the exact
+ * function, not bit for bit).  x_dtype bf16 or fp16; beta fp32 [C,16]
+ * (16-byte aligned); norm_weight, lin_weight [48, C], lin_bias fp32 or
+ * x_dtype; shift / scale rows [B, C] at row stride mod_ld, x_dtype.  s == 4,
+ * C % 256 == 0, G % 16 == 0, L <= 12, P*P*CO == 48, x0 below 4 GiB, img
+ * 16-byte aligned.  The caller workspace (256-byte aligned) holds M_b, Q_b's
+ * partial sums and the per-slab fp32 partial rows (3 KiB per cell and 256
+ * channels).
+ */
+size_t lthc_materialise_decoder_workspace_bytes(int64_t B, int64_t G, int64_t s, int64_t C);
+int lthc_materialise_decoder_fwd(const void* x0, int x_dtype, const void* const* dz, const void* const* beta,
+                                 int w_dtype, const void* norm_weight, int nw_dtype, const void* shift,
+                                 const void* scale, int64_t mod_ld, const void* lin_weight, int lw_dtype,
+                                 const void* lin_bias, int lb_dtype, void* img, int64_t B, int64_t G, int64_t s,
+                                 int64_t C, int L, int64_t P, int64_t CO, float eps, void* workspace,
+                                 size_t workspace_bytes, void* stream);
+
+/*
  * BATCHED WEIGHT CONVERSION (no reference op: autocast converts each fp32
  * weight in its own kernel on every forward).  entries: device array of
  * {const float* src; int64_t numel; int64_t dst_offset; int64_t first_block}
