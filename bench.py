@@ -427,8 +427,9 @@ def interface_forward(args, torch, dev, ops, B, G, C, L):
 def interface_c_level(args, torch, dev, B, G, C, L):
     """The whole-interface C entry points with every dZ_l given (lthc_interface_fwd, lthc_interface_bwd): one call
     each, no autograd, events around `steps` calls over two input sets.  Not the metric's step (the model's lazy
-    forward runs a branch between the recurrence steps); reported beside it.  Bytes: forward e(3T + (3L + 2)W)
-    (read, prefix recurrence e(W + 2LW), materialise).  Backward: the single-pass compulsory bytes e(3T + 3LW) (read
+    forward runs a branch between the recurrence steps); reported beside it.  Bytes: forward e(2T + (2L + 1)W), the
+    single-pass compulsory bytes (read X0 and the dZ stack; write X_L and Z_0 .. Z_L), which the one-pass kernel
+    moves.  Backward: the single-pass compulsory bytes e(3T + 3LW) (read
     G_L, X0, the H and dZ stacks; write dX0 and the dZ-gradient stack), against which the rate is reported; the
     implementation moves e(3T + 3LW + 2W): the tile kernel e(2T + 3LW + W) (it also writes S_0) and dalpha's pass
     over X0 and S_0 e(T + W)."""
@@ -490,14 +491,16 @@ def interface_c_level(args, torch, dev, B, G, C, L):
 
     fwd_ms, bwd_ms = timed(fwd), timed(bwd)
     T, W = B * H * H * C, B * G * G * C
-    fb = 2 * (3 * T + (3 * L + 2) * W)
+    fb = 2 * (2 * T + (2 * L + 1) * W)
     bb = 2 * (3 * T + 3 * L * W)
     out = {
         "workload": f"whole-interface C calls, every dZ_l given (B={B}, {H}x{H}/{G}x{G}, C={C}, L={L}, bf16, fp32 weights)",
         "timing": "events around consecutive calls, eager (several launches per call)",
         "fwd_ms": round(fwd_ms, 4),
         "fwd_bytes": fb,
+        "fwd_byte_definition": "single-pass compulsory e(2T + (2L + 1)W): X0 and the dZ stack read once, X_L and Z_0..Z_L written",
         "fwd_GBps": round(fb / (fwd_ms * 1e-3) / 1e9, 1),
+        "fwd_pct_of_peak_hbm": round(100.0 * fb / (fwd_ms * 1e-3) / PEAK_HBM, 2),
         "bwd_ms": round(bwd_ms, 4),
         "bwd_bytes": bb,
         "bwd_byte_definition": "single-pass compulsory e(3T + 3LW); the implementation moves e(3T + 3LW + 2W)",

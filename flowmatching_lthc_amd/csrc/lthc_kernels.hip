@@ -335,6 +335,7 @@ __global__ __launch_bounds__(kBlock) void read_fwd_kernel(const void* __restrict
 #pragma unroll
       for (int v = 0; v < VEC; ++v) acc[v] = fmaf(xv[v], a[v][k], acc[v]);
     }
+    hold_f32<DT>(acc);  // rounded once from fp32 (no mixed-precision fp16 fma with the last product)
     store_at<DT, VEC>(z, zo, acc);
   }
 }

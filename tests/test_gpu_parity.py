@@ -730,3 +730,32 @@ def test_interface_entry_points_bf16_configuration3_slice(coracle):
     for got, r, what in [(host(da), ref["alpha"], "dalpha")] + [(host(db[l]), ref["beta"][l], f"dbeta_{l}") for l in range(L)]:
         err = np.abs(got - r).max() / max(np.abs(r).max(), 1e-30)
         assert err <= 2e-2, f"{what}: {err:.3e}"
+
+
+@pytest.mark.parametrize("xdt", [BF16, torch.float16])
+@pytest.mark.parametrize(
+    "B,G,C,L,wdt",
+    [
+        (2, 16, 768, 12, F32),   # configuration 3's width and depth: the one-pass kernel
+        (2, 16, 256, 5, F32),    # padded depth bucket
+        (1, 8, 512, 3, None),    # weights in the activation dtype
+        (2, 4, 260, 3, F32),     # C not a multiple of 256: the composed form
+    ],
+)
+def test_interface_fwd_one_pass_equals_per_op_chain(B, G, C, L, xdt, wdt):
+    """lthc_interface_fwd reads X0 and each dZ_l once (iface_fwd_kernel) where the shape allows it.  Z_0 .. Z_L and
+    X_L equal, bit for bit, the per-op entry points it replaces: lthc_read_fwd, lthc_gamma (fp32), one lthc_recur_fwd
+    per step and lthc_materialise_fwd."""
+    wdt = wdt or xdt
+    print(f"case B={B} G={G} C={C} L={L} x={xdt} w={wdt}", flush=True)
+    d = cfg(B, G, C, L, seed=41 + L + C)
+    x0, alpha = dev(d["x0"], xdt), dev(d["alpha"], wdt)  # alpha and the betas share the weight dtype
+    betas, dzs = [dev(b, wdt) for b in d["beta"]], [dev(z, xdt) for z in d["dz"]]
+    zs, xl = capi.interface_fwd(x0, alpha, betas, dzs)
+    z = capi.read(x0, alpha)
+    gam = capi.gamma(alpha, betas)
+    assert torch.equal(zs[0], z), "Z_0 differs from lthc_read_fwd"
+    for l in range(L):
+        z = capi.recur(z, dzs[l], gam[l])
+        assert torch.equal(zs[l + 1], z), f"Z_{l + 1} differs from the recurrence steps"
+    assert torch.equal(xl, capi.materialise(x0, dzs, betas)), "X_L differs from lthc_materialise_fwd"
