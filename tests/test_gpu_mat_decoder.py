@@ -123,3 +123,28 @@ def test_model_fused_materialise_decoder_matches_unfused():
     e_u = (unfused - exact).abs().max().item() / scale
     print(f"  fused {e_f:.3e} unfused {e_u:.3e} of max|exact| {scale:.3f}")
     assert e_f <= 2e-2 and e_f <= max(1.5 * e_u, 1e-3)
+
+
+def test_materialise_decoder_graph_replay_equals_eager():
+    """The op under HIP-graph capture (its workspace from the graph's pool): every replay, with eager work and
+    synchronisations between replays, equals the eager result bit for bit."""
+    print("case graph replay", flush=True)
+    x0, dzs, betas, t2, nw, lw, lb = _inputs(2, 16, 768, 12, torch.bfloat16, torch.float32, seed=77)
+    shift, scale = t2.chunk(2, dim=1)
+    run = lambda: ops.final_accumulate_decoder_head(x0, dzs, betas, nw, shift, scale, lw, lb, 1e-6, 4)  # noqa: E731
+    eager = run()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        run()
+    torch.cuda.current_stream().wait_stream(s)
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        out = run()
+    for i in range(3):
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {i}"
+        other = ops.final_accumulate_decoder_head(x0 * 0.5, dzs, betas, nw, shift, scale, lw, lb, 1e-6, 4)  # eager work
+        torch.cuda.synchronize()
+        assert not torch.equal(other, eager)
