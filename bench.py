@@ -995,6 +995,7 @@ def main():
             "triangular_fwd_metric_shape": triangular_forward(args, torch, dev, B, G, C, L),
             "interface_c_level_metric_shape": interface_c_level(args, torch, dev, B, G, C, L),
             "interface_c_level_config3": interface_c_level(args, torch, dev, args.train_batch, G, C, L),
+            "interface_c_level_config5": interface_c_level(args, torch, dev, 32, 32, 1024, 24),
         }
 
     cpu = None

@@ -473,7 +473,7 @@ int lthc_read_bwd(const void* gz, const void* x, int x_dtype, const void* alpha,
  * with L <= 12 and C % 256 == 0 (one kernel writes z[0..L] and x_out, bitwise
  * the per-op entry points' values), and otherwise composes them (read, gamma,
  * recurrence prefix, materialise).  The backward is one pass over gx and the dz and gz
- * stacks for 16-bit activations with L <= 12, C % 64 == 0, G % 8 == 0 and
+ * stacks for 16-bit activations with L <= 24, C % 64 == 0, G % 8 == 0 and
  * 16-byte aligned gx, dx0 and alpha (one tile kernel writes ddz, dx0 and S_0
  * and the partial sums of dbeta's and the gamma terms; then dalpha's pass over
  * x0 and S_0), and otherwise a composition (materialise backward; the
