@@ -24,6 +24,7 @@
 #include <stdint.h>
 
 #include <algorithm>
+#include <initializer_list>
 #include <numeric>
 #include <string>
 #include <type_traits>
@@ -848,12 +849,12 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
 // 16 group sums are added in order g = 0..15 -- a fixed order, so the result
 // is bitwise reproducible, with 16x the parallelism of reduce_partials_kernel.
 constexpr int kRedGroups = 16;
-__global__ __launch_bounds__(256) void reduce_partials_split_kernel(const float* __restrict__ partial, int nparts,
-                                                                    int64_t n, void* __restrict__ out, int odt) {
+__device__ __forceinline__ void reduce_split_block(const float* __restrict__ partial, int nparts, int64_t n,
+                                                   int64_t cblock, void* __restrict__ out, int odt) {
   __shared__ float part[kRedGroups][16];
   const int col = threadIdx.x & 15;
   const int grp = threadIdx.x >> 4;
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 16 + col;
+  const int64_t i = cblock * 16 + col;
   float s = 0.f;
   if (i < n) {
     // loads in batches of 8 (in flight together), added in part order
@@ -875,6 +876,35 @@ __global__ __launch_bounds__(256) void reduce_partials_split_kernel(const float*
     for (int g = 0; g < kRedGroups; ++g) t += part[g][col];
     store_w(out, odt, i, t);
   }
+}
+
+__global__ __launch_bounds__(256) void reduce_partials_split_kernel(const float* __restrict__ partial, int nparts,
+                                                                    int64_t n, void* __restrict__ out, int odt) {
+  reduce_split_block(partial, nparts, n, blockIdx.x, out, odt);
+}
+
+// Several independent reductions in one launch (fp32 outputs), each segment's columns summed exactly as
+// reduce_partials_split_kernel sums them.  With 16 parts or fewer the group sums are single parts added in part
+// order, the order of reduce_partials_kernel, so every segment matches launch_reduce bit for bit.
+struct RedSeg {
+  const float* partial;
+  float* out;
+  int64_t n;
+  int64_t block0;  // first block of the segment
+  int nparts;
+};
+constexpr int kRedMaxSegs = 4;
+struct RedSegs {
+  RedSeg s[kRedMaxSegs];
+  int nseg;
+};
+
+__global__ __launch_bounds__(256) void reduce_partials_multi_kernel(RedSegs segs) {
+  const int64_t b = blockIdx.x;
+  int si = 0;
+  while (si + 1 < segs.nseg && b >= segs.s[si + 1].block0) ++si;
+  const RedSeg& sg = segs.s[si];
+  reduce_split_block(sg.partial, sg.nparts, sg.n, b - sg.block0, sg.out, LTHC_F32);
 }
 
 // ---------------------------------------------------------------------------
@@ -1282,6 +1312,19 @@ void launch_reduce(const float* partial, int nparts, int64_t n, void* out, hipSt
   } else {
     reduce_partials_split_kernel<<<static_cast<unsigned>((n + 15) / 16), 256, 0, st>>>(partial, nparts, n, out, odt);
   }
+}
+
+// The reductions of up to kRedMaxSegs (partial, nparts, n, out) segments in one launch.
+void launch_reduce_multi(std::initializer_list<RedSeg> list, hipStream_t st) {
+  RedSegs segs{};
+  int64_t blocks = 0;
+  for (const RedSeg& r : list) {
+    RedSeg& d = segs.s[segs.nseg++];
+    d = r;
+    d.block0 = blocks;
+    blocks += (r.n + 15) / 16;
+  }
+  reduce_partials_multi_kernel<<<static_cast<unsigned>(blocks), 256, 0, st>>>(segs);
 }
 
 template <int V>
