@@ -474,9 +474,9 @@ int lthc_read_bwd(const void* gz, const void* x, int x_dtype, const void* alpha,
  * the per-op entry points' values), and otherwise composes them (read, gamma,
  * recurrence prefix, materialise).  The backward is one pass over gx and the dz and gz
  * stacks for 16-bit activations with L <= 24, C % 64 == 0, G % 8 == 0 and
- * 16-byte aligned gx, dx0 and alpha (one tile kernel writes ddz, dx0 and S_0
- * and the partial sums of dbeta's and the gamma terms; then dalpha's pass over
- * x0 and S_0), and otherwise a composition (materialise backward; the
+ * 16-byte aligned gx, dx0, alpha and x0 (one tile kernel forms gamma, writes
+ * ddz, dx0 and S_0 and the partial sums of dbeta and of the gamma terms; then
+ * dalpha's pass over x0 and S_0 and one launch of the reductions), and otherwise a composition (materialise backward; the
  * recurrence steps in one pass over H, dZ and gdZ up to depth 24, one
  * lthc_recur_bwd or lthc_recur_bwd_sum per step above; read backward).  Both
  * give the per-step entry points' ddz and dx0 bit for bit (local_thc_triton_kernels.py:512-680,
