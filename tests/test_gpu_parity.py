@@ -709,6 +709,30 @@ def test_interface_bwd_one_pass_suffix_equals_per_step_chain(xdt, L, missing):
         assert err <= 1e-5, f"{what}: {err:.3e}"
 
 
+
+def test_interface_bwd_unaligned_x0_equals_aligned():
+    """An X0 that is 8- but not 16-byte aligned keeps lthc_interface_bwd off the tile kernel (its 16-byte X0 reads):
+    the composed form then gives the same dZ gradients and dX0 bit for bit, and the weight gradients to 1e-5."""
+    print("case unaligned x0", flush=True)
+    B, G, C, L = 2, 16, 256, 5
+    d = cfg(B, G, C, L, seed=77, grads=True)
+    x0 = dev(d["x0"], BF16)
+    buf = torch.empty(x0.numel() + 4, dtype=BF16, device=DEV)
+    x0u = buf[4:].view_as(x0)  # 8 bytes past a 16-byte boundary
+    x0u.copy_(x0)
+    assert x0u.data_ptr() % 16 == 8
+    alpha, betas = dev(d["alpha"]), [dev(b) for b in d["beta"]]
+    dzs, gx = [dev(z, BF16) for z in d["dz"]], dev(d["grad_xl"], BF16)
+    gzs = [dev(g, BF16) for g in d["grad_z"]]
+    got = capi.interface_bwd(gx, gzs, x0u, dzs, alpha, betas)
+    ref = capi.interface_bwd(gx, gzs, x0, dzs, alpha, betas)
+    assert torch.equal(got[0], ref[0]), "dX0"
+    for l in range(L):
+        assert torch.equal(got[1][l], ref[1][l]), f"d dZ_{l}"
+    for g, r, what in ((got[2], ref[2], "dalpha"), (got[3], ref[3], "dbeta")):
+        err = ((g - r).abs().max() / r.abs().max()).item()
+        assert err <= 1e-5, f"{what}: {err:.3e}"
+
 def test_interface_entry_points_bf16_configuration3_slice(coracle):
     """The whole-interface entry points at configuration 3's width and depth (B=4 slice, bf16, fp32 weights):
     X_L within one bf16 rounding of the oracle, gradients to the bf16 bar."""
