@@ -664,16 +664,17 @@ def test_interface_entry_points_match_closed_form_fp32(B, G, C, L, missing):
 
 @pytest.mark.parametrize("xdt", [BF16, torch.float16, F32])
 @pytest.mark.parametrize(
-    "L,missing",
-    [(12, ()), (12, (0, 11)), (12, (3, 4, 5)), (5, (2,)), (24, (7,)), (3, (1, 2))],
+    "L,missing,G",
+    [(12, (), 16), (12, (0, 11), 16), (12, (3, 4, 5), 16), (5, (2,), 16), (24, (7,), 16), (3, (1, 2), 16),
+     (12, (), 8), (24, (0,), 32)],  # one tile per cell row (G = 8); configuration 5's 32 x 32 workspace
 )
-def test_interface_bwd_one_pass_suffix_equals_per_step_chain(xdt, L, missing):
+def test_interface_bwd_one_pass_suffix_equals_per_step_chain(xdt, L, missing, G):
     """lthc_interface_bwd walks the recurrence backward of every step in one pass (recur_suffix_kernel, depth <= 24).
     Its dZ gradients and dX0 equal, bit for bit, the chain of per-step entry points it replaces: materialise
     backward, then l = L-1..0 one lthc_recur_bwd / lthc_recur_bwd_sum on the running suffix sum S_{l+1}, then
     S_0 = r(S_1 + H_0) and lthc_read_bwd.  The weight gradients sum in another order (relative 1e-5)."""
-    print(f"case x={xdt} L={L} missing={missing}", flush=True)
-    B, G, C = 2, 16, 256
+    print(f"case x={xdt} L={L} missing={missing} G={G}", flush=True)
+    B, C = 2, 256
     d = cfg(B, G, C, L, seed=31 + L, grads=True)
     x0, alpha = dev(d["x0"], xdt), dev(d["alpha"])
     betas, dzs = [dev(b) for b in d["beta"]], [dev(z, xdt) for z in d["dz"]]
