@@ -765,6 +765,8 @@ def test_interface_entry_points_bf16_configuration3_slice(coracle):
         (2, 16, 256, 5, F32),    # padded depth bucket
         (1, 8, 512, 3, None),    # weights in the activation dtype
         (2, 4, 260, 3, F32),     # C not a multiple of 256: the composed form
+        (1, 32, 256, 24, F32),   # configuration 5's depth and grid: the composed form
+        (2, 8, 192, 13, None),   # above depth 12, 16-bit weights: the composed form
     ],
 )
 def test_interface_fwd_one_pass_equals_per_op_chain(B, G, C, L, xdt, wdt):
