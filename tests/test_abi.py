@@ -70,6 +70,19 @@ def test_argument_errors_are_reported_without_launching():
     rc, msg = _err(lib.lthc_swiglu(ctypes.c_void_p(4096 + 8), _abi.BF16, fake, 16, 16, None))
     assert rc == _abi.ERR_INVALID and "aligned" in msg
 
+    # the whole-interface entry points: NULL arrays, a missing workspace (before any launch)
+    arrs = (ctypes.c_void_p * 12)(*([4096] * 12))
+    rc, msg = _err(lib.lthc_interface_bwd(fake, None, _abi.BF16, fake, arrs, fake, arrs, _abi.F32, fake, arrs, fake,
+                                          fake, 2, 16, 4, 768, 12, None, 0, None))  # fmt: skip
+    assert rc == _abi.ERR_INVALID and "NULL" in msg
+    rc, msg = _err(lib.lthc_interface_bwd(fake, arrs, _abi.BF16, fake, arrs, fake, arrs, _abi.F32, fake, arrs, fake,
+                                          fake, 2, 16, 4, 768, 12, None, 0, None))  # fmt: skip
+    assert rc == _abi.ERR_INVALID and "workspace" in msg
+    rc, msg = _err(lib.lthc_interface_fwd(fake, _abi.BF16, fake, arrs, _abi.F32, arrs, None, fake, 2, 16, 4, 768, 12,
+                                          None, 0, None))  # fmt: skip
+    assert rc == _abi.ERR_INVALID and "z (L + 1 outputs)" in msg
+    assert _abi.load().lthc_interface_workspace_bytes(2, 16, 4, 768, 0) == 0
+
 
 def test_workspace_sizes_are_consistent():
     n = _abi.weight_grad_workspace_bytes(256, 16, 4, 768, 12)
