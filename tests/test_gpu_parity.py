@@ -530,6 +530,37 @@ def test_hip_graph_replay_matches_eager():
         assert torch.equal(gb, gb_eager), f"replay {i}"
 
 
+
+def test_interface_bwd_graph_replay_matches_eager():
+    """lthc_interface_bwd (the single-pass tile kernel, the dalpha pass, the one-launch reductions and the gamma terms)
+    captured in a HIP graph: every replay, with eager work and synchronisations between replays, equals the eager call
+    bit for bit (the partial sums and counters need no clearing between calls)."""
+    print("case interface_bwd graph replay", flush=True)
+    B, G, C, L = 4, 16, 256, 12
+    d = cfg(B, G, C, L, seed=91, grads=True)
+    x0, alpha = dev(d["x0"], BF16), dev(d["alpha"])
+    betas, dzs = [dev(b) for b in d["beta"]], [dev(z, BF16) for z in d["dz"]]
+    gx = dev(d["grad_xl"], BF16)
+    gzs = [None if l == 3 else dev(g, BF16) for l, g in enumerate(d["grad_z"])]
+    eager = capi.interface_bwd(gx, gzs, x0, dzs, alpha, betas)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        capi.interface_bwd(gx, gzs, x0, dzs, alpha, betas)
+    torch.cuda.current_stream().wait_stream(s)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = capi.interface_bwd(gx, gzs, x0, dzs, alpha, betas)
+    flat = lambda r: [r[0], *r[1], r[2], r[3]]  # noqa: E731
+    for i in range(3):
+        other = capi.interface_bwd(gx, gzs, x0, [z * 0.5 for z in dzs], alpha, betas)  # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        for got, ref in zip(flat(out), flat(eager)):
+            assert torch.equal(got, ref), f"replay {i}"
+        assert not torch.equal(other[2], eager[2])
+
 # ---------------------------------------------------------------------------
 # final-layer RMSNorm + modulate (jit_thc::norm_modulate, the materialisation's consumer)
 # ---------------------------------------------------------------------------
