@@ -849,43 +849,50 @@ __global__ __launch_bounds__(256) void reduce_partials_kernel(const float* __res
 // 16 group sums are added in order g = 0..15 -- a fixed order, so the result
 // is bitwise reproducible, with 16x the parallelism of reduce_partials_kernel.
 constexpr int kRedGroups = 16;
+// A 256-thread block reduces COLS consecutive columns with 256 / COLS part groups: group g sums parts g, g + NG,
+// g + 2 NG, ... in order (NG = 256 / COLS), then the group sums are added in order g = 0..NG-1.  COLS = 16 gives 16
+// groups (narrow outputs: many partial rows over few columns); COLS = 64 makes a wavefront's load one 256-byte run
+// of a partial row (wide outputs).
+template <int COLS>
 __device__ __forceinline__ void reduce_split_block(const float* __restrict__ partial, int nparts, int64_t n,
                                                    int64_t cblock, void* __restrict__ out, int odt) {
-  __shared__ float part[kRedGroups][16];
-  const int col = threadIdx.x & 15;
-  const int grp = threadIdx.x >> 4;
-  const int64_t i = cblock * 16 + col;
+  constexpr int NG = 256 / COLS;
+  __shared__ float part[NG][COLS];
+  const int col = threadIdx.x % COLS;
+  const int grp = threadIdx.x / COLS;
+  const int64_t i = cblock * COLS + col;
   float s = 0.f;
   if (i < n) {
     // loads in batches of 8 (in flight together), added in part order
     int p = grp;
-    for (; p + 7 * kRedGroups < nparts; p += 8 * kRedGroups) {
+    for (; p + 7 * NG < nparts; p += 8 * NG) {
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = partial[static_cast<int64_t>(p + j * kRedGroups) * n + i];
+      for (int j = 0; j < 8; ++j) v[j] = partial[static_cast<int64_t>(p + j * NG) * n + i];
 #pragma unroll
       for (int j = 0; j < 8; ++j) s += v[j];
     }
-    for (; p < nparts; p += kRedGroups) s += partial[static_cast<int64_t>(p) * n + i];
+    for (; p < nparts; p += NG) s += partial[static_cast<int64_t>(p) * n + i];
   }
   part[grp][col] = s;
   __syncthreads();
   if (grp == 0 && i < n) {
     float t = 0.f;
 #pragma unroll
-    for (int g = 0; g < kRedGroups; ++g) t += part[g][col];
+    for (int g = 0; g < NG; ++g) t += part[g][col];
     store_w(out, odt, i, t);
   }
 }
 
+template <int COLS>
 __global__ __launch_bounds__(256) void reduce_partials_split_kernel(const float* __restrict__ partial, int nparts,
                                                                     int64_t n, void* __restrict__ out, int odt) {
-  reduce_split_block(partial, nparts, n, blockIdx.x, out, odt);
+  reduce_split_block<COLS>(partial, nparts, n, blockIdx.x, out, odt);
 }
 
-// Several independent reductions in one launch (fp32 outputs), each segment's columns summed exactly as
-// reduce_partials_split_kernel sums them.  With 16 parts or fewer the group sums are single parts added in part
-// order, the order of reduce_partials_kernel, so every segment matches launch_reduce bit for bit.
+// Several independent reductions in one launch (fp32 outputs), each segment's columns summed as
+// reduce_partials_split_kernel<16> sums them (16-column blocks: the 64-column form measured slower here, where
+// the segments have few partial rows).
 struct RedSeg {
   const float* partial;
   float* out;
@@ -904,7 +911,7 @@ __global__ __launch_bounds__(256) void reduce_partials_multi_kernel(RedSegs segs
   int si = 0;
   while (si + 1 < segs.nseg && b >= segs.s[si + 1].block0) ++si;
   const RedSeg& sg = segs.s[si];
-  reduce_split_block(sg.partial, sg.nparts, sg.n, b - sg.block0, sg.out, LTHC_F32);
+  reduce_split_block<16>(sg.partial, sg.nparts, sg.n, b - sg.block0, sg.out, LTHC_F32);
 }
 
 // ---------------------------------------------------------------------------
@@ -1309,8 +1316,10 @@ int64_t recur_bwd_blocks_y(int64_t rows) { return std::min((rows + 4 * kRU - 1) 
 void launch_reduce(const float* partial, int nparts, int64_t n, void* out, hipStream_t st, int odt = LTHC_F32) {
   if (nparts <= kRedGroups) {
     reduce_partials_kernel<<<static_cast<unsigned>((n + 255) / 256), 256, 0, st>>>(partial, nparts, n, out, odt);
+  } else if (n >= 64 * 256) {  // wide: 64-column blocks (a wavefront's load is one 256-byte run of a partial row)
+    reduce_partials_split_kernel<64><<<static_cast<unsigned>((n + 63) / 64), 256, 0, st>>>(partial, nparts, n, out, odt);
   } else {
-    reduce_partials_split_kernel<<<static_cast<unsigned>((n + 15) / 16), 256, 0, st>>>(partial, nparts, n, out, odt);
+    reduce_partials_split_kernel<16><<<static_cast<unsigned>((n + 15) / 16), 256, 0, st>>>(partial, nparts, n, out, odt);
   }
 }
 
