@@ -190,8 +190,6 @@ def c_oracle_baseline(G, C, L, budget_s):
     """The C oracle (fp32 in/out, fp64 accumulate, OpenMP) on a configuration-2 slice of the workload: a secondary
     CPU figure beside the reference's op sequence."""
     sys.path.insert(0, ROOT)
-    import numpy as np
-
     from oracle import oracle as O
 
     if not os.path.exists(O.LIB):

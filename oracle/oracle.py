@@ -75,13 +75,6 @@ def to_cells(x: np.ndarray, g: int) -> np.ndarray:
     return x.reshape(b, g, s, g, s, c).transpose(0, 1, 3, 2, 4, 5).reshape(b, g * g, s * s, c)
 
 
-def from_cells(xc: np.ndarray, g: int) -> np.ndarray:
-    """Cell view [B, G*G, S*S, C] -> NHWC [B,H,H,C]."""
-    b, _, k, c = xc.shape
-    s = math.isqrt(k)
-    return xc.reshape(b, g, g, s, s, c).transpose(0, 1, 3, 2, 4, 5).reshape(b, g * s, g * s, c)
-
-
 # ---------------------------------------------------------------------------
 # numpy restatement (float64), following the reference's eager op sequence
 # ---------------------------------------------------------------------------

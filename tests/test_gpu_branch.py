@@ -11,9 +11,6 @@ move one rounding.  Gradients (recomputed through the eager sequence) equal the 
 
 from __future__ import annotations
 
-import math
-
-import numpy as np
 import pytest
 import torch
 

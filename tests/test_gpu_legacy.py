@@ -8,7 +8,6 @@ modules (local_thc.py:511-617), against the CPU oracle's read / write / weight-g
 
 from __future__ import annotations
 
-import numpy as np
 import pytest
 import torch
 
