@@ -429,6 +429,101 @@ __global__ __launch_bounds__(kBlock) void cell_mat_kernel(const void* __restrict
 }
 
 // ---------------------------------------------------------------------------
+// DEEP WHOLE-CELL MATERIALISE (depth 17-24 with a base, tensors below 4 GiB):
+// cell_mat_kernel's thread (one channel x all 16 taps) for depths whose
+// 16 x LMAX weights do not fit in VGPRs beside a cell's loads.  Layers
+// 0..LV-1 keep their weights in VGPRs; layers LV..LMAX-1 are staged once per
+// block into LDS as [layer][tap quad][channel] float4 rows, so a wavefront's
+// read of one quad is 64 consecutive 16-byte lanes (no bank conflicts).
+// Block = 4 wavefronts on one 64-channel slab, wavefront w on cell 4 b + w
+// of each grid step (gridDim.x * 4 cells, a multiple of G): each dz run is
+// requested once per cell, where cell_mat_kernel's two tap groups request it
+// twice at these depths.  Same FMA order and roundings as cell_mat_kernel:
+// acc = base, acc = fma(beta_l, dz_l, acc) for l = 0..L-1, one rounding.  When
+// L < LMAX (EXACT == false) the padding layers' dz and beta entries point at
+// layer 0 (filled in by the launcher, so the kernel indexes the pointer packs
+// directly) and they contribute a selected 0, as in cell_mat_kernel; the
+// layer count is re-read in every cell iteration, so the compiler does not
+// hold a mask per layer across the loop (they spilled scalar registers).
+// ---------------------------------------------------------------------------
+template <int DT, int WDT, int LMAX, int LV, bool EXACT>
+__global__ __launch_bounds__(kBlock, 2) void cell_mat_deep_kernel(const void* __restrict__ base, PtrPack dz,
+                                                                  PtrPack beta, void* __restrict__ out, int L,
+                                                                  uint32_t ncells, int G, int C) {
+  constexpr int ES = Fmt<DT>::bytes;
+  constexpr int LD = LMAX - LV;  // layers whose weights sit in LDS
+  static_assert(LD >= 1 && LV >= 1, "layer split");
+  __shared__ float4 wl[LD][kK / 4][64];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int c0 = blockIdx.y * 64 + lane;
+  const bool live = c0 < C;  // every thread takes part in the staging and its barrier
+#pragma unroll
+  for (int j = 0; j < LD; ++j) {  // wavefront w stages tap quad w of every LDS layer
+    const int l = LV + j;
+    float v[4] = {0.f, 0.f, 0.f, 0.f};
+    if (live) load_wvec<WDT, 4>(beta.p[l], static_cast<int64_t>(c0) * kK + 4 * w, v);
+    wl[j][w][lane] = make_float4(v[0], v[1], v[2], v[3]);
+  }
+  float bw[LV][kK];
+#pragma unroll
+  for (int l = 0; l < LV; ++l) {
+#pragma unroll
+    for (int k = 0; k < kK; ++k) bw[l][k] = 0.f;
+    if (live) load_wvec<WDT, kK>(beta.p[l], static_cast<int64_t>(c0) * kK, bw[l]);
+  }
+  __syncthreads();
+  uint32_t cell = blockIdx.x * 4 + w;
+  if (!live || cell >= ncells) return;
+  const uint32_t tap_b = C * ES;
+  const uint32_t row_b = G * kS * tap_b;
+  const uint32_t P = gridDim.x * 4;
+  const uint32_t step_x = (P / G) * kS * row_b;
+  const uint32_t step_z = P * tap_b;
+  uint32_t xo = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES);
+  uint32_t zo = (cell * C + c0) * ES;
+  for (; cell < ncells; cell += P, xo += step_x, zo += step_z) {
+    Raw<DT, 1> xr[kK];
+    Raw<DT, 1> dr[LMAX];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) load_at<DT, 1, true>(base, xo + (k / kS) * row_b + (k % kS) * tap_b, xr[k]);
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) load_at<DT, 1>(dz.p[l], zo, dr[l]);
+    LTHC_PHASE_BARRIER();
+
+    float acc[kK][1];
+#pragma unroll
+    for (int k = 0; k < kK; ++k) unpack_raw<DT, 1>(xr[k], acc[k]);
+    int Lc = L;
+    if constexpr (!EXACT) asm volatile("" : "+s"(Lc));
+#pragma unroll
+    for (int l = 0; l < LMAX; ++l) {
+      float d[1];
+      unpack_raw<DT, 1>(dr[l], d);
+      if constexpr (!EXACT) d[0] = l < Lc ? d[0] : 0.f;
+      if (l < LV) {
+#pragma unroll
+        for (int k = 0; k < kK; ++k) acc[k][0] = fmaf(bw[l < LV ? l : 0][k], d[0], acc[k][0]);
+      } else {
+#pragma unroll
+        for (int q = 0; q < kK / 4; ++q) {
+          const float4 b = wl[l >= LV ? l - LV : 0][q][lane];
+          acc[4 * q + 0][0] = fmaf(b.x, d[0], acc[4 * q + 0][0]);
+          acc[4 * q + 1][0] = fmaf(b.y, d[0], acc[4 * q + 1][0]);
+          acc[4 * q + 2][0] = fmaf(b.z, d[0], acc[4 * q + 2][0]);
+          acc[4 * q + 3][0] = fmaf(b.w, d[0], acc[4 * q + 3][0]);
+        }
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < kK; ++k) {
+      hold_f32<DT>(acc[k]);
+      store_at<DT, 1, true>(out, xo + (k / kS) * row_b + (k % kS) * tap_b, acc[k]);
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // MATERIALISE / WRITE: out[cell,k,c] = base[cell,k,c] + sum_l beta_l[c,k] dz_l[cell,c]
 // Thread = CPT channels x TPT taps of one tap row; its LMAX x CPT x TPT write
 // weights stay in VGPRs.  Block = 256 threads = QS channel groups x NTG tap
@@ -1516,9 +1611,40 @@ void launch_cell_mat(const void* base, const PtrPack& dz, const PtrPack& beta, v
                                                                     static_cast<uint32_t>(ncells), G, C);
 }
 
+// Layers whose weights the deep materialisation keeps in VGPRs: 242 VGPRs at depth 24, two wavefronts per SIMD (with
+// 12 layers it spilled; 6 and 8 measured slower on MI355X).
+constexpr int kDeepRegLayers = 10;
+
+template <int DT, int WDT, int LMAX, bool EXACT>
+void launch_cell_mat_deep(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells,
+                          int G, int C, hipStream_t st) {
+  constexpr int LV = kDeepRegLayers;
+  const auto kernel = cell_mat_deep_kernel<DT, WDT, LMAX, LV, EXACT>;
+  static const int per_cu = resident_blocks(kernel);
+  const int slabs = (C + 63) / 64;
+  const int64_t per = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu * 4 / slabs, ncells, G, 4);
+  PtrPack dp = dz, bp = beta;  // padding layers: layer 0's rows (contributing a selected 0)
+  for (int l = L; l < LMAX; ++l) {
+    dp.p[l] = dz.p[0];
+    bp.p[l] = beta.p[0];
+  }
+  kernel<<<dim3(static_cast<unsigned>(per / 4), slabs), kBlock, 0, st>>>(base, dp, bp, out, L,
+                                                                        static_cast<uint32_t>(ncells), G, C);
+}
+
 template <int DT, int WDT, int LMAX>
 void launch_cell_mat_l(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells,
                        int G, int C, hipStream_t st) {
+  // depths 17-24 with a base: the deep kernel, which requests each dz run once per cell (5-6 % faster at depth 24
+  // on configuration 5's shape, bitwise equal).  At depth 16 it was faster at C = 768 and slower at C = 1024 (where
+  // cell_mat_kernel's two tap groups run three wavefronts per SIMD), and without a base it spilled.
+  if constexpr (LMAX == 24) {
+    if (base != nullptr) {
+      if (L == LMAX) launch_cell_mat_deep<DT, WDT, LMAX, true>(base, dz, beta, out, L, ncells, G, C, st);
+      else launch_cell_mat_deep<DT, WDT, LMAX, false>(base, dz, beta, out, L, ncells, G, C, st);
+      return;
+    }
+  }
   if (base == nullptr) {  // the sum of writes alone (the adjoint of a multi-weight read)
     if (L == LMAX) launch_cell_mat<DT, WDT, LMAX, false, true>(base, dz, beta, out, L, ncells, G, C, st);
     else launch_cell_mat<DT, WDT, LMAX, false, false>(base, dz, beta, out, L, ncells, G, C, st);

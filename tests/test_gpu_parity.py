@@ -428,6 +428,29 @@ def test_edge_shapes_fp32(coracle, B, G, C, L):
     assert_f32(host(gam), coracle.Cgamma(d["alpha"], list(d["beta"])), tol=1e-6, what="gamma")
 
 
+# Depths 17-24 with a base run the deep whole-cell kernel (the weights of layers 10 and up staged in LDS): ragged
+# channel slabs (C % 64 != 0), workspace grids that its 4 cells per block do not divide, padded depths (L < 24) and
+# each activation / weight pair.
+@pytest.mark.parametrize(
+    "B,G,C,L,xdt,wdt",
+    [(1, 2, 8, 17, F32, F32), (2, 6, 100, 24, BF16, F32), (1, 5, 68, 21, torch.float16, torch.float16),
+     (2, 16, 256, 23, BF16, BF16), (3, 3, 192, 24, F32, F32), (1, 4, 64, 19, torch.float16, F32)],
+)  # fmt: skip
+def test_deep_materialise(coracle, B, G, C, L, xdt, wdt):
+    d = cfg(B, G, C, L, seed=B * G + C + L)
+    x0 = dev(d["x0"], xdt)
+    betas = [dev(b, wdt) for b in d["beta"]]
+    dzs = [dev(z, xdt) for z in d["dz"]]
+    got = host(capi.materialise(x0, dzs, betas))
+    ref = coracle.Cwrite(host(x0), [host(z) for z in dzs], [host(b) for b in betas])
+    if xdt == F32:
+        assert_f32(got, ref, what="materialise")
+    else:  # one rounding of the fp32 sum
+        ulp = 2.0**-11 if xdt == torch.float16 else 2.0**-8
+        err = np.abs(got - ref)
+        assert (err <= ulp * np.abs(ref) + 1e-6).all(), f"rounding bound violated: {err.max()}"
+
+
 @pytest.mark.parametrize("xdt,wdt", [(torch.float16, torch.float16), (torch.float16, F32), (BF16, BF16)])
 def test_16bit_activations_and_weights(coracle, xdt, wdt):
     d = cfg(2, 16, 768, 3)
