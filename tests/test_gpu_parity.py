@@ -327,6 +327,23 @@ def test_config5_shape_bf16(coracle):
     assert_f32(host(capi.weight_grad(g, dzs)), coracle.Cweight_grad(gh, dzh, G), what="gbeta")
 
 
+def test_config5_full_batch_materialise_bf16(coracle):
+    """Configuration 5 at its full batch (B=32: every grid step of the deep materialisation): samples 0, 17 and 31
+    against the C oracle, and dZ = 0 giving X0 back bit for bit."""
+    B, G, C, L = 32, 32, 1024, 24
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    x0 = torch.randn((B, 4 * G, 4 * G, C), generator=gen, device=DEV).to(BF16)
+    betas = [torch.randn((C, 16), generator=gen, device=DEV) * 0.02 for _ in range(L)]
+    dzs = [(torch.randn((B, G * G, C), generator=gen, device=DEV) * 0.02).to(BF16) for _ in range(L)]
+    out = capi.materialise(x0, dzs, betas)
+    bh = [host(b) for b in betas]
+    for b in (0, 17, B - 1):
+        ref = coracle.Cwrite(host(x0[b : b + 1]), [host(z[b : b + 1]) for z in dzs], bh)
+        assert_bf16(host(out[b : b + 1]), ref, what=f"materialise sample {b}")
+    zeros = [torch.zeros_like(z) for z in dzs[:1]] * L
+    assert torch.equal(capi.materialise(x0, zeros, betas), x0)
+
+
 @pytest.mark.parametrize(
     "B,G,C,L,xdt,wdt",
     [
