@@ -1,5 +1,7 @@
-"""Benchmark configuration 3 at its own size (B=64, 64x64 / 16x16, C=768, L=12, bf16 activations, fp32 weights):
-the interface forward + backward through the model's autograd ops and through the single-pass C entry point
+"""Benchmark configurations 3 and 5 at their own sizes, bf16 activations, fp32 weights:
+  configuration 3: B=64, 64x64 / 16x16, C=768, L=12;
+  configuration 5: B=32, 128x128 / 32x32, C=1024, L=24 (the depth-24 kernels over every grid step).
+The interface forward + backward through the model's autograd ops and through the single-pass C entry point
 (lthc_interface_bwd), each against the closed-form backward evaluated by the C oracle on the same bf16 inputs.
 
 Closed form (local_thc.py:1211-1223, 1325-1328, 1368-1372 differentiated; G = dL/dX_L, H_l = dL/dZ_l,
@@ -12,8 +14,8 @@ the gamma-term sums run in float64 here.
 Bounds, in units of the reference's largest magnitude (the gradients are O(1e-3)): the GPU path rounds the suffix
 sums, the recurrence gradients and its outputs to bf16 and the model path uses the bf16 gamma of the autograd
 sequence, so activation gradients are held to max |d| <= 1e-2 max|ref| and mean |d| <= 4e-3 mean|ref| (one bf16 unit roundoff), weight
-gradients (fp32 sums over 16384 cells of bf16 products) to max |d| <= 1e-2 max|ref|.  A dropped term (the gamma
-term, the base G in dX0, a layer of the suffix) moves them by O(1).
+gradients (fp32 sums over 16384 or 32768 cells of bf16 products) to max |d| <= 1e-2 max|ref|.  A dropped term (the
+gamma term, the base G in dX0, a layer of the suffix) moves them by O(1).
 """
 
 import ctypes
@@ -26,18 +28,19 @@ from flowmatching_lthc_amd import _abi, ops
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-B, G, C, L = 64, 16, 768, 12
 BF16 = torch.bfloat16
+CONFIGS = {"configuration3": (64, 16, 768, 12, 3), "configuration5": (32, 32, 1024, 24, 5)}  # B, G, C, L, seed
 
 
-@pytest.fixture(scope="module")
-def config3(coracle):
-    """Configuration 3's draws (X0 ~ N(0,1), alpha ~ N(1/16, 0.01), beta_l ~ N(0, 0.02), dZ_l ~ N(0, 0.02), G_L and
+@pytest.fixture(scope="module", params=list(CONFIGS))
+def full(request, coracle):
+    """The configuration's draws (X0 ~ N(0,1), alpha ~ N(1/16, 0.01), beta_l ~ N(0, 0.02), dZ_l ~ N(0, 0.02), G_L and
     H_l ~ N(0, 1e-3)) from a seeded generator on the device (the host copies are the same bits), and the closed-form
     reference on the host."""
-    print("case configuration 3: B=64 inputs and closed-form reference", flush=True)
+    B, G, C, L, seed = CONFIGS[request.param]
+    print(f"case {request.param}: B={B} G={G} C={C} L={L} inputs and closed-form reference", flush=True)
     coracle.set_threads(min(16, coracle.max_threads()))
-    gen = torch.Generator(device=DEV).manual_seed(3)
+    gen = torch.Generator(device=DEV).manual_seed(seed)
     rn = lambda *shape: torch.randn(shape, generator=gen, device=DEV)  # noqa: E731
     t = {
         "x0": rn(B, 4 * G, 4 * G, C).to(BF16).cpu(),
@@ -66,7 +69,7 @@ def config3(coracle):
     gw = coracle.Cweight_grad(gx, dzs, G)
     ref["beta"] = [gw[l] + dgam[l][:, None] * alpha for l in range(L)]
     ref["alpha"] = coracle.Cweight_grad(x0, [S[0]], G)[0] + sum(dgam[l][:, None] * betas[l] for l in range(L))
-    return t, ref
+    return (B, G, C, L), t, ref
 
 
 def _check(name, got, ref, act):
@@ -80,10 +83,11 @@ def _check(name, got, ref, act):
 
 
 @pytest.mark.timeout(600)
-def test_configuration3_autograd_backward_b64(config3):
+def test_autograd_backward_full_size(full):
     """The model's lazy-forward ops (read_with_residual, the one-launch bf16 gamma, the split recurrence steps, the
-    12-pointer materialisation) and torch.autograd.grad over (X_L, Z_0..Z_11), as bench.py's training leg runs."""
-    t, ref = config3
+    12-pointer materialisation at depth 12 and the list op otherwise) and torch.autograd.grad over
+    (X_L, Z_0..Z_{L-1}), as bench.py's training leg runs."""
+    (B, G, C, L), t, ref = full
     x0 = t["x0"].to(DEV).requires_grad_()
     alpha = t["alpha"].to(DEV).requires_grad_()
     betas = [b.to(DEV).requires_grad_() for b in t["beta"]]
@@ -95,7 +99,7 @@ def test_configuration3_autograd_backward_b64(config3):
         z, zb, dv = ops.lazy_workspace_step(z, dzs[l], gam[l], split=True)
         zs.append(zb)
         dzv.append(dv)
-    xl = ops.final_accumulate_b4_12_traceable(x0v, *dzv, *betas)
+    xl = ops.final_accumulate_b4_12_traceable(x0v, *dzv, *betas) if L == 12 else ops.final_accumulate_list(x0v, dzv, betas)
     grads = torch.autograd.grad([xl] + zs[:L], [x0, alpha] + betas + dzs, [t["gx"].to(DEV)] + [g.to(DEV) for g in t["gz"]])
     torch.cuda.synchronize()
     _check("dX0", grads[0], ref["x0"], True)
@@ -106,9 +110,9 @@ def test_configuration3_autograd_backward_b64(config3):
 
 
 @pytest.mark.timeout(300)
-def test_configuration3_single_pass_backward_b64(config3):
-    """lthc_interface_bwd (the single-pass tile kernel, then dalpha and the gamma terms) at configuration 3."""
-    t, ref = config3
+def test_single_pass_backward_full_size(full):
+    """lthc_interface_bwd (the single-pass tile kernel, then dalpha and the gamma terms) at the configuration's size."""
+    (B, G, C, L), t, ref = full
     lib = _abi.load()
     x0, gx = t["x0"].to(DEV), t["gx"].to(DEV)
     dzs, gzs = [z.to(DEV) for z in t["dz"]], [g.to(DEV) for g in t["gz"]]
