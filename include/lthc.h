@@ -470,9 +470,9 @@ int lthc_read_bwd(const void* gz, const void* x, int x_dtype, const void* alpha,
  *             dalpha = sum x0 S_0 + sum_l (sum S_{l+1} dz_l) beta_l
  *             (dalpha [C,16], dbeta [L,C,16] fp32; fixed-order reductions).
  * The forward is one pass over x0 and the dz stack for 16-bit activations
- * with L <= 12 and C % 256 == 0 (one kernel writes z[0..L] and x_out, bitwise
- * the per-op entry points' values), and otherwise composes them (read, gamma,
- * recurrence prefix, materialise).  The backward is one pass over gx and the dz and gz
+ * with L <= 12 and C % 256 == 0, or L == 24 and any C (one kernel writes
+ * z[0..L] and x_out, bitwise the per-op entry points' values), and otherwise
+ * composes them (read, gamma, recurrence prefix, materialise).  The backward is one pass over gx and the dz and gz
  * stacks for 16-bit activations with L <= 24, C % 64 == 0, G % 8 == 0 and
  * 16-byte aligned gx, dx0, alpha and x0 (one tile kernel forms gamma, writes
  * ddz, dx0 and S_0 and the partial sums of dbeta and of the gamma terms; then

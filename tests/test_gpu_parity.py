@@ -836,14 +836,15 @@ def test_interface_entry_points_bf16_configuration3_slice(coracle):
         (2, 16, 256, 5, F32),    # padded depth bucket
         (1, 8, 512, 3, None),    # weights in the activation dtype
         (2, 4, 260, 3, F32),     # C not a multiple of 256: the composed form
-        (1, 32, 256, 24, F32),   # configuration 5's depth and grid: the composed form
-        (2, 8, 192, 13, None),   # above depth 12, 16-bit weights: the composed form
+        (1, 32, 256, 24, F32),   # configuration 5's depth and grid: the one-pass depth-24 kernel
+        (2, 6, 100, 24, None),   # depth 24, ragged channel slab, grid not a multiple of 4 cells, 16-bit weights
+        (2, 8, 192, 13, None),   # padded depths above 12: the composed form
     ],
 )
 def test_interface_fwd_one_pass_equals_per_op_chain(B, G, C, L, xdt, wdt):
-    """lthc_interface_fwd reads X0 and each dZ_l once (iface_fwd_kernel) where the shape allows it.  Z_0 .. Z_L and
-    X_L equal, bit for bit, the per-op entry points it replaces: lthc_read_fwd, lthc_gamma (fp32), one lthc_recur_fwd
-    per step and lthc_materialise_fwd."""
+    """lthc_interface_fwd reads X0 and each dZ_l once (iface_fwd_kernel, iface_fwd_deep_kernel at depth 24) where the
+    shape allows it.  Z_0 .. Z_L and X_L equal, bit for bit, the per-op entry points it replaces: lthc_read_fwd,
+    lthc_gamma (fp32), one lthc_recur_fwd per step and lthc_materialise_fwd."""
     wdt = wdt or xdt
     print(f"case B={B} G={G} C={C} L={L} x={xdt} w={wdt}", flush=True)
     d = cfg(B, G, C, L, seed=41 + L + C)
