@@ -736,23 +736,27 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
 
 
 def recurrence_cache_leg(args, torch, ops, sets, alpha, beta_stack, L, W, step_ms, step_bytes):
-    """The step's L recurrence launches timed one by one with events, as they run in the step (Z_l written by the
-    previous launch just before: served partly from the 256 MB MALL) and with Z_l and dZ_l evicted first (an
-    untimed 1 GiB streaming fill before each launch, as a transformer branch between the steps would).  Reports
-    both rates and the step time the cold launches imply: step_ms + sum_l (cold_l - warm_l)."""
+    """The step's L recurrence launches timed one by one with events: as they run in the step (Z_l written by the
+    previous launch just before), with Z_l and dZ_l evicted from the 256 MB MALL by an untimed 1 GiB read sweep
+    before each launch (both then come from HBM), and after an untimed 1 GiB streaming fill instead (the same
+    eviction, plus the fill's dirty lines written back while the launch runs).  Reports the three rates and the step
+    time each cold form implies: step_ms + sum_l (cold_l - in_step_l)."""
     stream = torch.cuda.current_stream()
-    flush = torch.empty((1 << 30) // 4, device=sets[0][0].device, dtype=torch.float32)
+    sweep = torch.ones((1 << 30) // 4, device=sets[0][0].device, dtype=torch.float32)
+    sink = torch.zeros((), device=sweep.device, dtype=torch.float32)
     reps = max(2, min(args.steps, 10))
 
-    def run(cold):
+    def run(evict):
         ev = []
         for i in range(reps):
             x0, dzs = sets[i % 2]
             z = ops.local_write_traceable(x0, alpha)
             gam = ops.lazy_gamma_stack(alpha, beta_stack)
             for l in range(L):
-                if cold:
-                    flush.fill_(float(l))
+                if evict == "read":
+                    sink.add_(sweep.sum())
+                elif evict == "write":
+                    sweep.fill_(float(l))
                 e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
                 e0.record(stream)
                 z = ops.lazy_workspace_update(z, dzs[l], gam[l])
@@ -761,21 +765,33 @@ def recurrence_cache_leg(args, torch, ops, sets, alpha, beta_stack, L, W, step_m
         torch.cuda.synchronize()
         return sum(a.elapsed_time(b) for a, b in ev) / len(ev)
 
-    run(True)  # warm-up of both paths
-    warm_ms, cold_ms = run(False), run(True)
-    del flush
+    run("read")  # warm-up of every path
+    run("write")
+    warm_ms, read_ms, write_ms = run(None), run("read"), run("write")
+    del sweep
     rb = 2 * 3 * W  # bytes per launch: Z_l and dZ_l in, Z_{l+1} out (bf16; gamma negligible)
-    cold_step = step_ms + L * (cold_ms - warm_ms)
+
+    def implied(ms):
+        step = step_ms + L * (ms - warm_ms)
+        return round(step, 4), round(100.0 * step_bytes / (step * 1e-3) / PEAK_HBM, 2)
+
+    read_step, read_pct = implied(read_ms)
+    write_step, write_pct = implied(write_ms)
     return {
         "per_launch_us_in_step_order": round(warm_ms * 1e3, 2),
         "per_launch_GBps_in_step_order": round(rb / (warm_ms * 1e-3) / 1e9, 1),
-        "per_launch_us_mall_cold": round(cold_ms * 1e3, 2),
-        "per_launch_GBps_mall_cold": round(rb / (cold_ms * 1e-3) / 1e9, 1),
-        "step_ms_implied_mall_cold": round(cold_step, 4),
-        "pct_of_peak_hbm_implied_mall_cold": round(100.0 * step_bytes / (cold_step * 1e-3) / PEAK_HBM, 2),
+        "per_launch_us_hbm_cold": round(read_ms * 1e3, 2),
+        "per_launch_GBps_hbm_cold": round(rb / (read_ms * 1e-3) / 1e9, 1),
+        "step_ms_implied_hbm_cold": read_step,
+        "pct_of_peak_hbm_implied_hbm_cold": read_pct,
+        "per_launch_us_after_write_fill": round(write_ms * 1e3, 2),
+        "per_launch_GBps_after_write_fill": round(rb / (write_ms * 1e-3) / 1e9, 1),
+        "step_ms_implied_after_write_fill": write_step,
+        "pct_of_peak_hbm_implied_after_write_fill": write_pct,
         "note": "the headline value times the step as launched back to back, where each recurrence launch reads the "
-        "Z_l that the previous launch wrote microseconds earlier; with a branch between the steps (the model) Z_l "
-        "comes from HBM: this leg evicts it with a 1 GiB fill before every launch",
+        "Z_l that the previous launch wrote microseconds earlier; hbm_cold evicts Z_l and dZ_l with a 1 GiB read "
+        "sweep before every launch (both then come from HBM); after_write_fill evicts them with a 1 GiB fill, whose "
+        "dirty lines are written back to HBM during the launch",
     }
 
 
