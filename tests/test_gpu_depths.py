@@ -1,0 +1,66 @@
+"""Every depth the C ABI takes, through the per-op entry points, against the oracle (MI355X only).
+
+The materialisation and its backward pick a kernel by depth bucket: the whole-cell kernel with its weights in
+VGPRs for depths 1, 2, 4, 8 and 12 (exact and padded buckets), two tap groups for depths 13-16, the deep kernel
+with part of its weights in LDS for depths 17-24 with a base, and the block-range kernels above depth 24.  The
+backward's tile kernel has 4 wavefronts up to depth 12 and 8 above.  This sweep runs each depth from 1 to 25, plus
+33 and 48 (the largest the ABI takes), on one sample of the B/4 geometry (G = 16) at C = 256, and checks:
+- lthc_materialise_fwd with and without a base against X0 + sum_l P_l dZ_l (local_thc.py:1368-1372;
+  local_thc_triton_kernels.py:317-405), the oracle evaluated in float64 on the bf16-rounded inputs;
+- lthc_materialise_bwd's gdZ_l = sum_k beta_l G and gbeta_l = sum_cells G dZ_l
+  (local_thc_triton_kernels.py:512-680);
+- lthc_read_multi_fwd and lthc_weight_grad, the same two quantities from the per-op kernels.
+Tolerances as in test_gpu_parity: bf16 outputs within one rounding of the fp64 value (and 2e-2 absolute), fp32
+weight gradients within 1e-5 of max|ref|.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import oracle as O
+
+from . import capi
+from .test_gpu_parity import BF16, F32, assert_bf16, assert_f32, dev, host, rounded
+
+pytestmark = pytest.mark.gpu
+
+DEPTHS = list(range(1, 26)) + [33, 48]
+
+
+@pytest.mark.parametrize("L", DEPTHS)
+def test_every_depth_materialise_and_backward(L):
+    B, G, C = 1, 16, 256
+    print(f"case depth L={L} B={B} G={G} C={C} bf16 activations, fp32 weights", flush=True)
+    d = O.make_inputs(B, G, C, L, seed=100 + L, grads=True)
+    x0h = rounded(d["x0"], BF16)
+    dzh = [rounded(d["dz"][l], BF16) for l in range(L)]
+    gh = rounded(d["grad_xl"], BF16)
+    betas_np = [d["beta"][l] for l in range(L)]
+
+    x0 = dev(x0h, BF16)
+    dzs = [dev(z, BF16) for z in dzh]
+    gr = dev(gh, BF16)
+    betas = [dev(b, F32) for b in betas_np]
+
+    ref = O.final_accumulate_np(x0h, dzh, betas_np)
+    assert_bf16(host(capi.materialise(x0, dzs, betas)), ref, what=f"materialise L={L}")
+    if L <= 24:  # a NULL base takes up to 24 layers (the adjoint of the multi-weight read)
+        ref0 = O.final_accumulate_np(np.zeros_like(x0h), dzh, betas_np)
+        assert_bf16(host(capi.materialise(None, dzs, betas)), ref0, what=f"materialise without base L={L}")
+
+    gdz, gb = capi.materialise_bwd(gr, dzs, betas)
+    multi = capi.read_multi(gr, betas)
+    wg = capi.weight_grad(gr, dzs)
+    for l in range(L):
+        ref_gdz = O.read_np(gh, betas_np[l], G)
+        assert_bf16(host(gdz[l]), ref_gdz, what=f"materialise_bwd gdZ_{l} L={L}")
+        assert_bf16(host(multi[l]), ref_gdz, what=f"read_multi gdZ_{l} L={L}")
+        ref_gb = O.weight_grad_np(gh, dzh[l], G)
+        assert_f32(host(gb[l]), ref_gb, what=f"materialise_bwd gbeta_{l} L={L}")
+        assert_f32(host(wg[l]), ref_gb, what=f"weight_grad gbeta_{l} L={L}")
+    # the two backward paths share their FMA order for gdZ: bitwise equal
+    for l in range(L):
+        assert torch.equal(gdz[l], multi[l]), f"materialise_bwd and read_multi gdZ_{l} differ at L={L}"
