@@ -1,4 +1,4 @@
-"""Every depth the C ABI takes, through the per-op entry points, against the oracle (MI355X only).
+"""Every depth the C ABI takes, through the per-op and whole-interface entry points, against the oracle (MI355X only).
 
 The materialisation and its backward pick a kernel by depth bucket: the whole-cell kernel with its weights in
 VGPRs for depths 1, 2, 4, 8 and 12 (exact and padded buckets), two tap groups for depths 13-16, the deep kernel
@@ -64,3 +64,48 @@ def test_every_depth_materialise_and_backward(L):
     # the two backward paths share their FMA order for gdZ: bitwise equal
     for l in range(L):
         assert torch.equal(gdz[l], multi[l]), f"materialise_bwd and read_multi gdZ_{l} differ at L={L}"
+
+
+def assert_grad(got, ref, what, weight=False):
+    """Bounds of tests/test_gpu_full_size.py: the bf16 path rounds the suffix sums and its outputs, so activation
+    gradients are held to max|d| <= 1e-2 max|ref| and mean|d| <= 4e-3 mean|ref|, fp32 weight gradients to
+    max|d| <= 1e-2 max|ref|; a dropped term moves them by O(1)."""
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    d = np.abs(got - ref)
+    assert d.max() <= 1e-2 * np.abs(ref).max(), f"{what}: max|d| {d.max():.3e} vs max|ref| {np.abs(ref).max():.3e}"
+    if not weight:
+        assert d.mean() <= 4e-3 * np.abs(ref).mean(), f"{what}: mean|d| {d.mean():.3e} vs mean|ref| {np.abs(ref).mean():.3e}"
+
+
+@pytest.mark.parametrize("L", list(range(1, 26)) + [33])
+def test_every_depth_whole_interface(L):
+    """lthc_interface_fwd (one pass at depths <= 12 and 24, composed at the padded depths 13-23 and above 24) and
+    lthc_interface_bwd (the single-pass tile kernel up to depth 24, the composed chain above) at every depth:
+    Z_0 = R(X0), each step Z_{l+1} = Z_l + gamma_l dZ_l from the returned bf16 Z_l (local_thc.py:1211-1223,
+    1325-1328), X_L (:1368-1372), and the closed-form backward (oracle.interface_bwd_np) on the same bf16 inputs."""
+    B, G, C = 1, 16, 256
+    print(f"case whole interface L={L} B={B} G={G} C={C} bf16 activations, fp32 weights", flush=True)
+    d = O.make_inputs(B, G, C, L, seed=200 + L, grads=True)
+    x0h = rounded(d["x0"], BF16)
+    dzh = [rounded(d["dz"][l], BF16) for l in range(L)]
+    gxh = rounded(d["grad_xl"], BF16)
+    gzh = [rounded(d["grad_z"][l], BF16) for l in range(L)]
+    alpha_np, betas_np = d["alpha"], [d["beta"][l] for l in range(L)]
+    x0, gx = dev(x0h, BF16), dev(gxh, BF16)
+    dzs, gzs = [dev(z, BF16) for z in dzh], [dev(z, BF16) for z in gzh]
+    alpha, betas = dev(alpha_np, F32), [dev(b, F32) for b in betas_np]
+
+    zs, xl = capi.interface_fwd(x0, alpha, betas, dzs)
+    assert_bf16(host(zs[0]), O.read_np(x0h, alpha_np, G), what=f"Z_0 L={L}")
+    for l in range(L):
+        ref = O.lazy_update_np(host(zs[l]), dzh[l], O.gamma_np(alpha_np, betas_np[l]))
+        assert_bf16(host(zs[l + 1]), ref, what=f"Z_{l + 1} L={L}")
+    assert_bf16(host(xl), O.final_accumulate_np(x0h, dzh, betas_np), what=f"X_L L={L}")
+
+    dx0, ddz, da, db = capi.interface_bwd(gx, gzs, x0, dzs, alpha, betas)
+    ref = O.interface_bwd_np(x0h, alpha_np, dzh, betas_np, gxh, gzh, G)
+    assert_grad(host(dx0), ref["x0"], f"dX0 L={L}")
+    assert_grad(host(da), ref["alpha"], f"dalpha L={L}", weight=True)
+    for l in range(L):
+        assert_grad(host(ddz[l]), ref["dz"][l], f"d dZ_{l} L={L}")
+        assert_grad(host(db[l]), ref["beta"][l], f"dbeta_{l} L={L}", weight=True)
