@@ -4,14 +4,15 @@ The materialisation and its backward pick a kernel by depth bucket: the whole-ce
 VGPRs for depths 1, 2, 4, 8 and 12 (exact and padded buckets), two tap groups for depths 13-16, the deep kernel
 with part of its weights in LDS for depths 17-24 with a base, and the block-range kernels above depth 24.  The
 backward's tile kernel has 4 wavefronts up to depth 12 and 8 above.  This sweep runs each depth from 1 to 25, plus
-33 and 48 (the largest the ABI takes), on one sample of the B/4 geometry (G = 16) at C = 256, and checks:
+33 and 48 (the largest the ABI takes), on one sample of the B/4 geometry (G = 16) at C = 256, with bf16 activations
+and fp32 weights (the released autocast run), fp16 activations and weights, and fp32 throughout, and checks:
 - lthc_materialise_fwd with and without a base against X0 + sum_l P_l dZ_l (local_thc.py:1368-1372;
-  local_thc_triton_kernels.py:317-405), the oracle evaluated in float64 on the bf16-rounded inputs;
+  local_thc_triton_kernels.py:317-405), the oracle evaluated in float64 on the rounded inputs;
 - lthc_materialise_bwd's gdZ_l = sum_k beta_l G and gbeta_l = sum_cells G dZ_l
   (local_thc_triton_kernels.py:512-680);
 - lthc_read_multi_fwd and lthc_weight_grad, the same two quantities from the per-op kernels.
-Tolerances as in test_gpu_parity: bf16 outputs within one rounding of the fp64 value (and 2e-2 absolute), fp32
-weight gradients within 1e-5 of max|ref|.
+Tolerances as in test_gpu_parity: 16-bit outputs within one rounding of the fp64 value (and 2e-2 absolute), fp32
+outputs and weight gradients within 1e-5 of max|ref|.
 """
 
 from __future__ import annotations
@@ -30,34 +31,54 @@ pytestmark = pytest.mark.gpu
 DEPTHS = list(range(1, 26)) + [33, 48]
 
 
-@pytest.mark.parametrize("L", DEPTHS)
-def test_every_depth_materialise_and_backward(L):
-    B, G, C = 1, 16, 256
-    print(f"case depth L={L} B={B} G={G} C={C} bf16 activations, fp32 weights", flush=True)
-    d = O.make_inputs(B, G, C, L, seed=100 + L, grads=True)
-    x0h = rounded(d["x0"], BF16)
-    dzh = [rounded(d["dz"][l], BF16) for l in range(L)]
-    gh = rounded(d["grad_xl"], BF16)
-    betas_np = [d["beta"][l] for l in range(L)]
+F16 = torch.float16
 
-    x0 = dev(x0h, BF16)
-    dzs = [dev(z, BF16) for z in dzh]
-    gr = dev(gh, BF16)
-    betas = [dev(b, F32) for b in betas_np]
+
+def assert_act(got, ref, xdt, what):
+    """16-bit outputs within one rounding of the fp64 value (|d| <= u|ref| + 1e-5, u = 2^-8 for bf16 and 2^-11 for
+    fp16, and 2e-2 absolute); fp32 outputs within 1e-5 of max|ref|."""
+    if xdt == F32:
+        assert_f32(got, ref, what=what)
+        return
+    if xdt == BF16:
+        assert_bf16(got, ref, what=what)
+        return
+    got, ref = np.asarray(got, np.float64), np.asarray(ref, np.float64)
+    d = np.abs(got - ref)
+    assert d.max() <= 2e-2, f"{what}: max abs err {d.max():.3e} > 2e-2"
+    bad = int((d > 2.0**-11 * np.abs(ref) + 1e-5).sum())
+    assert bad == 0, f"{what}: {bad} elements exceed 2^-11|ref| + 1e-5"
+
+
+@pytest.mark.parametrize("xdt,wdt", [(BF16, F32), (F16, F16), (F32, F32)], ids=["bf16-f32w", "f16-f16w", "f32"])
+@pytest.mark.parametrize("L", DEPTHS)
+def test_every_depth_materialise_and_backward(L, xdt, wdt):
+    B, G, C = 1, 16, 256
+    print(f"case depth L={L} B={B} G={G} C={C} activations {xdt}, weights {wdt}", flush=True)
+    d = O.make_inputs(B, G, C, L, seed=100 + L, grads=True)
+    x0h = rounded(d["x0"], xdt)
+    dzh = [rounded(d["dz"][l], xdt) for l in range(L)]
+    gh = rounded(d["grad_xl"], xdt)
+    betas_np = [rounded(d["beta"][l], wdt) for l in range(L)]
+
+    x0 = dev(x0h, xdt)
+    dzs = [dev(z, xdt) for z in dzh]
+    gr = dev(gh, xdt)
+    betas = [dev(b, wdt) for b in betas_np]
 
     ref = O.final_accumulate_np(x0h, dzh, betas_np)
-    assert_bf16(host(capi.materialise(x0, dzs, betas)), ref, what=f"materialise L={L}")
+    assert_act(host(capi.materialise(x0, dzs, betas)), ref, xdt, what=f"materialise L={L}")
     if L <= 24:  # a NULL base takes up to 24 layers (the adjoint of the multi-weight read)
         ref0 = O.final_accumulate_np(np.zeros_like(x0h), dzh, betas_np)
-        assert_bf16(host(capi.materialise(None, dzs, betas)), ref0, what=f"materialise without base L={L}")
+        assert_act(host(capi.materialise(None, dzs, betas)), ref0, xdt, what=f"materialise without base L={L}")
 
     gdz, gb = capi.materialise_bwd(gr, dzs, betas)
     multi = capi.read_multi(gr, betas)
     wg = capi.weight_grad(gr, dzs)
     for l in range(L):
         ref_gdz = O.read_np(gh, betas_np[l], G)
-        assert_bf16(host(gdz[l]), ref_gdz, what=f"materialise_bwd gdZ_{l} L={L}")
-        assert_bf16(host(multi[l]), ref_gdz, what=f"read_multi gdZ_{l} L={L}")
+        assert_act(host(gdz[l]), ref_gdz, xdt, what=f"materialise_bwd gdZ_{l} L={L}")
+        assert_act(host(multi[l]), ref_gdz, xdt, what=f"read_multi gdZ_{l} L={L}")
         ref_gb = O.weight_grad_np(gh, dzh[l], G)
         assert_f32(host(gb[l]), ref_gb, what=f"materialise_bwd gbeta_{l} L={L}")
         assert_f32(host(wg[l]), ref_gb, what=f"weight_grad gbeta_{l} L={L}")
