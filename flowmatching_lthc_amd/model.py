@@ -167,6 +167,36 @@ class BottleneckPatchEmbedNHWC(nn.Module):
         return F.linear(h, w2.view(self.proj2.out_channels, -1), b2)
 
 
+class DirectPatchEmbedNHWC(nn.Module):
+    """One conv patchify (in -> C, kernel = stride = patch), NHWC out (local_thc.py:92-119), as one GEMM over the
+    patch rows in NHWC order (the conv's weight is a linear map of each patch in channel, row, column order)."""
+
+    def __init__(
+        self,
+        img_size: int = 256,
+        patch_size: int = 4,
+        in_chans: int = 3,
+        bottleneck_dim: int = 128,
+        embed_dim: int = 768,
+        bias: bool = True,
+    ) -> None:
+        super().__init__()
+        self.img_size = (img_size, img_size)
+        self.patch_size = (patch_size, patch_size)
+        self.grid_size = (img_size // patch_size, img_size // patch_size)
+        self.num_patches = self.grid_size[0] * self.grid_size[1]
+        self.proj = nn.Conv2d(in_chans, embed_dim, kernel_size=patch_size, stride=patch_size, bias=bias)
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        if tuple(x.shape[-2:]) != self.img_size:
+            raise ValueError(f"expected image size {self.img_size}, got {tuple(x.shape[-2:])}")
+        b, cin = x.shape[:2]
+        p = self.patch_size[0]
+        gh, gw = self.grid_size
+        patches = x.reshape(b, cin, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5).reshape(b, gh, gw, cin * p * p)
+        return F.linear(patches, self.proj.weight.view(self.proj.out_channels, -1), self.proj.bias)
+
+
 class TimestepEmbedder(nn.Module):
     """Sinusoidal timestep features (cos then sin) through a 2-layer SiLU MLP (local_thc.py:175-200)."""
 
@@ -371,6 +401,40 @@ class FinalLayerSharedAdaLN(nn.Module):
     def forward(self, x: torch.Tensor, t2: torch.Tensor) -> torch.Tensor:
         shift, scale = t2.chunk(2, dim=1)
         return self.linear(norm_modulate(self.norm_final, x, shift, scale))
+
+
+class WorkspaceJiTBranch(WorkspaceSharedAdaLNBranch):
+    """The workspace branch with its own AdaLN head (local_thc.py:270-297): t6 = adaLN_modulation(c), then the
+    shared-AdaLN branch's attention + SwiGLU update."""
+
+    def __init__(
+        self,
+        hidden_size: int,
+        num_heads: int,
+        mlp_ratio: float = 4.0,
+        attn_drop: float = 0.0,
+        proj_drop: float = 0.0,
+        attn_backend: str = "flash",
+    ) -> None:
+        super().__init__(hidden_size, num_heads, mlp_ratio, attn_drop, proj_drop, attn_backend)
+        self.adaLN_modulation = nn.Sequential(nn.SiLU(), CastLinear(hidden_size, 6 * hidden_size, bias=True))
+
+    def forward(self, z: torch.Tensor, c: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> torch.Tensor:
+        return self.forward_with_modulation(z, self.adaLN_modulation(c), rope)
+
+    def forward_with_modulation(self, z: torch.Tensor, t6: torch.Tensor, rope: VisionRotaryEmbeddingFast) -> torch.Tensor:
+        return super().forward(z, t6, rope)
+
+
+class FinalLayer(FinalLayerSharedAdaLN):
+    """The decoder with its own AdaLN head (local_thc.py:853-862): (shift, scale) = adaLN_modulation(c)."""
+
+    def __init__(self, hidden_size: int, patch_size: int, out_channels: int) -> None:
+        super().__init__(hidden_size, patch_size, out_channels)
+        self.adaLN_modulation = nn.Sequential(nn.SiLU(), CastLinear(hidden_size, 2 * hidden_size, bias=True))
+
+    def forward(self, x: torch.Tensor, c: torch.Tensor) -> torch.Tensor:
+        return super().forward(x, self.adaLN_modulation(c))
 
 
 class SharedReadLocalTHCSharedAdaLNJiTBlock(nn.Module):
@@ -814,17 +878,30 @@ LocalTHC_JiT_models = {
     "SharedWrite-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_LocalTHC_SharedAdaLN_JiT_B_4,
 }
 
-MODEL_NAMES = (
+_SHARED_READ_NAMES = (
     "lthc_b4_velocity",
     "local_thc_jit_shared_read_fused_final12_shared_adaln_b4",
     "local_thc_jit_shared_write_fused_final12_shared_adaln_b4",
 )
+# registry name -> LocalTHCV2_JiT_models key (flowmatching_lthc/models/__init__.py:29-36)
+_V2_NAMES = {
+    "local_thc_v2_fused_final12_shared_adaln_b4": "LocalTHCv2-FusedFinal12-SharedAdaLN-JiT-B/4",
+    "local_thc_v2_fused_final12_adaln_b4": "LocalTHCv2-FusedFinal12-AdaLN-JiT-B/4",
+    "local_thc_v2_direct_fused_final12_shared_adaln_b4": "LocalTHCv2-Direct-FusedFinal12-SharedAdaLN-JiT-B/4",
+    "local_thc_v2_direct_fused_final12_adaln_b4": "LocalTHCv2-Direct-FusedFinal12-AdaLN-JiT-B/4",
+}
+MODEL_NAMES = _SHARED_READ_NAMES + tuple(_V2_NAMES)
 
 
 def build_model(name: str = "lthc_b4_velocity", **kwargs) -> nn.Module:
-    """The released LTHC-B/4 shared-read fused-final12 model (flowmatching_lthc/models/__init__.py:17-28)."""
-    if name in MODEL_NAMES:
+    """The registry of the public release (flowmatching_lthc/models/__init__.py:17-38): the LTHC-B/4 shared-read
+    fused-final12 model under its three names, and the four v2 models (``model_v2``)."""
+    if name in _SHARED_READ_NAMES:
         return LocalTHC_JiT_models["SharedRead-FusedFinal12-LocalTHC-SharedAdaLN-JiT-B/4"](**kwargs)
+    if name in _V2_NAMES:
+        from .model_v2 import LocalTHCV2_JiT_models
+
+        return LocalTHCV2_JiT_models[_V2_NAMES[name]](**kwargs)
     if name in LocalTHC_JiT_models:
         return LocalTHC_JiT_models[name](**kwargs)
     raise ValueError(f"unknown model: {name}; available={MODEL_NAMES + tuple(LocalTHC_JiT_models)}")
