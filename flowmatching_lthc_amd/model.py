@@ -840,6 +840,16 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
                 m.__dict__.pop("_cast", None)
 
 
+class SharedReadFusedFinalLocalTHCSharedAdaLNJiT(SharedReadLocalTHCSharedAdaLNJiT):
+    """Any-depth form whose materialisation is the stacked op over [L,B,M,C] dZ and [L,C,16] write weights
+    (local_thc.py:1397-1410)."""
+
+    def final_accumulate_reference(self, x0: torch.Tensor, dz_list: list[torch.Tensor]) -> torch.Tensor:
+        dz_stack = torch.stack(dz_list, dim=0).contiguous()
+        beta_stack = torch.stack([blk.write.write_weight for blk in self.blocks], dim=0).contiguous()
+        return ops.final_accumulate_b4_traceable(x0, dz_stack, beta_stack)
+
+
 class SharedReadFusedFinal12LocalTHCSharedAdaLNJiT(SharedReadLocalTHCSharedAdaLNJiT):
     """Depth-12 form whose materialisation is the 12-pointer op (local_thc.py:1413-1420)."""
 
@@ -853,6 +863,7 @@ class SharedReadFusedFinal12LocalTHCSharedAdaLNJiT(SharedReadLocalTHCSharedAdaLN
 # Old class names (local_thc.py:1428-1431).
 SharedWriteLocalTHCSharedAdaLNJiTBlock = SharedReadLocalTHCSharedAdaLNJiTBlock
 SharedWriteLocalTHCSharedAdaLNJiT = SharedReadLocalTHCSharedAdaLNJiT
+SharedWriteFusedFinalLocalTHCSharedAdaLNJiT = SharedReadFusedFinalLocalTHCSharedAdaLNJiT
 SharedWriteFusedFinal12LocalTHCSharedAdaLNJiT = SharedReadFusedFinal12LocalTHCSharedAdaLNJiT
 
 
@@ -860,6 +871,13 @@ def SharedRead_FusedFinal12_LocalTHC_SharedAdaLN_JiT_B_4(**kwargs) -> SharedRead
     """LTHC-B/4: patch 4, hidden 768, depth 12, 12 heads, bottleneck 128, 16x16 workspace (local_thc.py:1705-1719)."""
     kwargs.setdefault("pool_groups", 768)
     return SharedReadFusedFinal12LocalTHCSharedAdaLNJiT(
+        patch_size=4, hidden_size=768, depth=12, num_heads=12, bottleneck_dim=128, workspace_grid=16, **kwargs
+    )
+
+
+def SharedRead_FusedFinal_LocalTHC_SharedAdaLN_JiT_B_4(**kwargs) -> SharedReadFusedFinalLocalTHCSharedAdaLNJiT:
+    kwargs.setdefault("pool_groups", 768)
+    return SharedReadFusedFinalLocalTHCSharedAdaLNJiT(
         patch_size=4, hidden_size=768, depth=12, num_heads=12, bottleneck_dim=128, workspace_grid=16, **kwargs
     )
 
@@ -874,6 +892,8 @@ def SharedRead_LocalTHC_SharedAdaLN_JiT_B_4(**kwargs) -> SharedReadLocalTHCShare
 LocalTHC_JiT_models = {
     "SharedRead-FusedFinal12-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_FusedFinal12_LocalTHC_SharedAdaLN_JiT_B_4,
     "SharedWrite-FusedFinal12-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_FusedFinal12_LocalTHC_SharedAdaLN_JiT_B_4,
+    "SharedRead-FusedFinal-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_FusedFinal_LocalTHC_SharedAdaLN_JiT_B_4,
+    "SharedWrite-FusedFinal-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_FusedFinal_LocalTHC_SharedAdaLN_JiT_B_4,
     "SharedRead-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_LocalTHC_SharedAdaLN_JiT_B_4,
     "SharedWrite-LocalTHC-SharedAdaLN-JiT-B/4": SharedRead_LocalTHC_SharedAdaLN_JiT_B_4,
 }

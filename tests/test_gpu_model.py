@@ -212,3 +212,29 @@ def test_b4_configuration4_b64_matches_fp32_reference():
     assert err <= 2e-2, err
     assert err <= max(1.5 * err_eager, 1e-3), (err, err_eager)
     assert rel(ours32, exact) <= 1e-4
+
+
+def test_stacked_fused_final_model_equals_fused_final12():
+    """SharedRead-FusedFinal (the stacked materialisation op, local_thc.py:1397-1410) and SharedRead-FusedFinal12
+    (the 12-pointer op, :1413-1420) compute the same X_L: with the same weights the two models agree, fp32 and
+    under bf16 autocast, forward and read-weight gradient."""
+    print("case stacked vs 12-pointer fused-final model, B=2", flush=True)
+    m12 = M.randomize_parameters(M.build_model("SharedRead-FusedFinal12-LocalTHC-SharedAdaLN-JiT-B/4"), seed=21).to(DEV)
+    ms = M.build_model("SharedRead-FusedFinal-LocalTHC-SharedAdaLN-JiT-B/4").to(DEV)
+    ms.load_state_dict(m12.state_dict())
+    assert type(ms).final_accumulate_reference is not type(m12).final_accumulate_reference
+    gen = torch.Generator(device=DEV).manual_seed(22)
+    x = torch.randn((2, 3, 256, 256), generator=gen, device=DEV)
+    t = torch.rand((2,), generator=gen, device=DEV)
+    y = torch.randint(0, 1000, (2,), generator=gen, device=DEV)
+    m12.fused_materialise_decoder = False  # both models then decode the materialised X_L the same way
+    outs = {}
+    for key, m in (("12", m12), ("stack", ms)):
+        m.zero_grad(set_to_none=True)
+        out = m(x, t, y)
+        (out * out).sum().backward()
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            out16 = m(x, t, y)
+        outs[key] = (out.detach(), out16.float(), m.shared_read.read_logits.grad.clone(), m.blocks[4].write.write_weight.grad.clone())
+    for a, b, what in zip(outs["12"], outs["stack"], ("fp32 out", "bf16 out", "read_logits grad", "write_weight grad")):
+        assert rel(a, b) <= 1e-6, (what, rel(a, b))
