@@ -262,6 +262,62 @@ def eager_interface(model, torch):
     return model
 
 
+def model_train_steps(args, torch, dev):
+    """The reference's training-step benchmark (bench/benchmark_lthc_v2.py:15-62) on this build: per model, bf16
+    parameters in train mode, SGD(lr=0), images/targets [B,3,256,256] bf16 ~ N(0,1), t ~ U(0,1), labels uniform in
+    [0,1000); one step = zero_grad, forward under bf16 autocast, fp32 MSE loss, backward, optimizer step; warm-up,
+    then `model_steps` timed steps between two synchronisations (wall clock, as the reference times them).
+    Models: the released lthc_b4_velocity and the v2 shared-AdaLN model (its triangular interface)."""
+    import time
+
+    from flowmatching_lthc_amd import model as M
+
+    B = args.model_batch
+    out = {}
+    for name in ("lthc_b4_velocity", "local_thc_v2_fused_final12_shared_adaln_b4"):
+        torch.manual_seed(123)
+        model = M.build_model(name).to(device=dev, dtype=torch.bfloat16).train()
+        opt = torch.optim.SGD(model.parameters(), lr=0.0)
+        gen = torch.Generator(device=dev).manual_seed(3)
+        x = torch.randn((B, 3, 256, 256), generator=gen, device=dev, dtype=torch.bfloat16)
+        target = torch.randn((B, 3, 256, 256), generator=gen, device=dev, dtype=torch.bfloat16)
+        t = torch.rand((B,), generator=gen, device=dev)
+        y = torch.randint(0, 1000, (B,), generator=gen, device=dev)
+
+        def step():
+            opt.zero_grad(set_to_none=True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                pred = model(x, t, y)
+                loss = (pred.float() - target.float()).square().mean()
+            loss.backward()
+            opt.step()
+            return loss
+
+        torch.cuda.reset_peak_memory_stats()
+        for _ in range(args.warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.model_steps):
+            loss = step()
+        torch.cuda.synchronize()
+        step_s = (time.perf_counter() - t0) / args.model_steps
+        out[name] = {
+            "step_ms": round(step_s * 1e3, 3),
+            "samples_per_s": round(B / step_s, 1),
+            "peak_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
+            "loss": float(loss.detach()),
+        }
+        del model, opt, x, target
+        torch.cuda.empty_cache()
+    return {
+        "workload": "training step as bench/benchmark_lthc_v2.py times it (bf16 parameters, autocast, MSE, SGD lr=0), eager",
+        "batch": B,
+        "steps": args.model_steps,
+        "models": out,
+    }
+
+
 def model_forward(args, torch, dev, compare=True):
     """LTHC-B/4 forward, random-init weights, bf16 autocast, images [B,3,256,256] ~ N(0,1), t ~ U(0,1), labels
     uniform in [0,1000).  Timed eagerly and as one HIP graph replayed per forward (static inputs; the replay
@@ -1002,6 +1058,7 @@ def main():
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     model_fwd = None if args.no_model else model_forward(args, torch, dev)
+    model_train = None if args.no_model else model_train_steps(args, torch, dev)
     train = None if args.no_train else interface_train(args, torch, dev, ops)
     configs = None
     if not args.no_configs:
@@ -1061,6 +1118,7 @@ def main():
         "cpu_baseline": cpu,
         "recurrence_mall": recur_cache,
         "model_fwd": model_fwd,
+        "model_train": model_train,
         "interface_train": train,
         "configs": configs,
         "extra": {
