@@ -27,9 +27,19 @@ from .model import migrate_lthc_state_dict_keys
 CHECKPOINT_KEYS = ("model", "optimizer", "ema", "step", "args", "meta")
 
 
-def migrate_checkpoint_state(state: Mapping[str, torch.Tensor]) -> dict[str, torch.Tensor]:
-    """State dict with the current read / write key names (flowmatching_lthc/checkpoint.py:12-14)."""
-    return migrate_lthc_state_dict_keys(dict(state))
+def migrate_checkpoint_state(state: Mapping[str, torch.Tensor], keep: set[str] | None = None) -> dict[str, torch.Tensor]:
+    """State dict with the current read / write key names (flowmatching_lthc/checkpoint.py:12-14).
+
+    Keys in ``keep`` (the target model's own names) are left as they are.  The migration renames every
+    ``.read_weight`` to ``.write_weight``, which is right for the old shared-read checkpoints but would fold a
+    v2 model's ``pool.read_weight`` onto its ``pool.write_weight``; the reference's loader does that (a v2
+    checkpoint then fails to load strictly, and its EMA read weights are silently not loaded)."""
+    state = dict(state)
+    if not keep:
+        return migrate_lthc_state_dict_keys(state)
+    out = migrate_lthc_state_dict_keys({k: v for k, v in state.items() if k not in keep})
+    out.update({k: v for k, v in state.items() if k in keep})
+    return out
 
 
 def load_checkpoint(path: str | os.PathLike, map_location: str | torch.device = "cpu") -> dict:
@@ -45,17 +55,18 @@ def load_model_state(model: torch.nn.Module, ckpt: Mapping, key: str = "ema") ->
 
     ``key="model"`` loads the full state dict strictly.  ``key="ema"`` takes every entry the EMA holds (the
     EMA stores parameters only) and keeps the model's own values for the rest, such as buffers; the names
-    kept are returned.  Old key names are migrated first.  Raises ``ValueError`` for another key and
-    ``KeyError`` when the checkpoint has no EMA weights.
+    kept are returned.  Old key names are migrated first (names the model itself has are kept as they are).
+    Raises ``ValueError`` for another key and ``KeyError`` when the checkpoint has no EMA weights.
     """
+    own = set(model.state_dict())
     if key == "model":
-        model.load_state_dict(migrate_checkpoint_state(ckpt["model"]))
+        model.load_state_dict(migrate_checkpoint_state(ckpt["model"], own))
         return []
     if key != "ema":
         raise ValueError(f"unsupported checkpoint state key: {key}")
     if "ema" not in ckpt:
         raise KeyError("checkpoint does not contain EMA weights")
-    ema = migrate_checkpoint_state(ckpt["ema"])
+    ema = migrate_checkpoint_state(ckpt["ema"], own)
     state = model.state_dict()
     kept = []
     for name in state:

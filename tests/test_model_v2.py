@@ -87,3 +87,26 @@ def test_direct_patch_embed_matches_reference(fixture):
     close(out, f["out"])
     with pytest.raises(ValueError, match="expected image size"):
         embed(torch.zeros(1, 3, 16, 16))
+
+
+def test_v2_checkpoint_round_trip(tmp_path):
+    """A v2 checkpoint ({model, optimizer, ema, step, args, meta}) loads back, model and EMA: its pool.read_weight
+    keys are the model's own names and are not migrated onto pool.write_weight (the reference's loader folds
+    them together)."""
+    from flowmatching_lthc_amd import checkpoint as CK
+
+    src = M.randomize_parameters(M.build_model("local_thc_v2_fused_final12_adaln_b4"), seed=3)
+    opt = torch.optim.SGD(src.parameters(), lr=0.0)
+    ema = [p.detach() * 0.5 for p in src.parameters()]
+    path = tmp_path / "v2.pt"
+    CK.save_checkpoint(path, src, opt, ema, 7, {"model": "local_thc_v2_fused_final12_adaln_b4"})
+    ck = CK.load_checkpoint(path)
+    dst = M.build_model("local_thc_v2_fused_final12_adaln_b4")
+    assert CK.load_model_state(dst, ck, key="model") == []
+    for k, v in src.state_dict().items():
+        assert torch.equal(dst.state_dict()[k], v), k
+    assert not torch.equal(dst.blocks[0].pool.read_weight, dst.blocks[0].pool.write_weight)
+    dst2 = M.build_model("local_thc_v2_fused_final12_adaln_b4")
+    CK.load_model_state(dst2, ck, key="ema")
+    for (n, p), e in zip(dst2.named_parameters(), ema):
+        assert torch.equal(p.detach(), e), n
