@@ -95,3 +95,35 @@ def test_v2_gradients_match_torch_interface(name):
     for key, a, b in zip(params, got, ref):
         err = (a - b).abs().max().item() / max(b.abs().max().item(), 1e-30)
         assert err <= 1e-4, f"{key}: max|d|/max|ref| = {err:.3e}"
+
+
+def test_v2_forward_graph_replay_equals_eager():
+    """The v2 forward captured as one HIP graph (bases, active-prefix sums, materialisation, branch) replays to the
+    eager output bit for bit, several times with eager work in between."""
+    print("case v2 graph replay B=2 bf16 autocast", flush=True)
+    model = M.randomize_parameters(M.build_model(NAMES[0]), seed=15).to(DEV).eval()
+    gen = torch.Generator(device=DEV).manual_seed(16)
+    x = torch.randn((2, 3, 256, 256), generator=gen, device=DEV)
+    t = torch.rand((2,), generator=gen, device=DEV)
+    y = torch.randint(0, 1000, (2,), generator=gen, device=DEV)
+
+    def fwd():
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            return model(x, t, y)
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for _ in range(2):
+            fwd()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fwd()
+    eager = fwd().clone()
+    for _ in range(3):
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager)
+        fwd()
+        torch.cuda.synchronize()
