@@ -289,6 +289,36 @@ LTHC_DEV int64_t cell_hoff(int64_t cell, int G, int C) {
   return (r * (kS * kS) * G + (cell - r * G) * kS) * C;
 }
 
+// Grid-stride step of P cells over the NHWC tensor (byte offsets below 4 GiB)
+// for any P, not only multiples of G, so a grid can fill every resident slot.
+// P cells are P / G cell rows plus P % G cells; when the column of the current
+// cell passes G the step crosses one more cell row, which adds the 3 high-res
+// rows the column wrap skips (a cell row is 4 high-res rows, one of which the
+// G column steps already cover).  `cell` is wave-uniform in every caller, so
+// the column counter and the select live in scalar registers.
+struct CellStride {
+  uint32_t step_x;  // bytes of P / G cell rows plus P % G cells
+  uint32_t wrap_x;  // 3 high-res rows
+  uint32_t r;       // P % G
+  uint32_t gx;      // column of the current cell
+  uint32_t G;
+
+  LTHC_DEV CellStride(uint32_t P, uint32_t cell, int G_, uint32_t tap_b, uint32_t row_b) {
+    G = static_cast<uint32_t>(G_);
+    r = P % G;
+    gx = cell % G;
+    step_x = (P / G) * kS * row_b + r * kS * tap_b;
+    wrap_x = (kS - 1) * row_b;
+  }
+  // Bytes from the current cell to the one P cells on; moves the column.
+  LTHC_DEV uint32_t advance() {
+    gx += r;
+    const bool wrap = gx >= G;
+    gx = wrap ? gx - G : gx;
+    return step_x + (wrap ? wrap_x : 0u);
+  }
+};
+
 // ---------------------------------------------------------------------------
 // READ: z[cell, c] = sum_k alpha[c,k] x[cell, k, c]
 // Thread = VEC channels of one cell, all 16 taps; alpha for those channels
@@ -351,9 +381,9 @@ __global__ __launch_bounds__(kBlock) void read_fwd_kernel(const void* __restrict
 // wavefront lies in one tap group, so each dz run is requested once per tap
 // group (once per cell when TG = 1) and every wavefront access is a
 // contiguous 64 * CPT-element run of one tap.  Cells are visited grid-stride
-// with gridDim.x % G == 0 and gridDim.x * gridDim.y no larger than the
-// resident block count, so the whole grid sweeps one compact window of cells
-// at a time with no tail round.  When L < LMAX (EXACT == false) the padding
+// with gridDim.x * gridDim.y equal to the resident block count (any gridDim.x:
+// CellStride steps the offsets), so the whole grid sweeps one compact window
+// of cells at a time with no tail round.  When L < LMAX (EXACT == false) the padding
 // layers load layer 0 and contribute a selected 0.
 // Accumulation: acc = base, acc = fma(beta_l, dz_l, acc) for l = 0..L-1
 // (local_thc_triton_kernels.py:367-403).  Base reads and output writes are
@@ -381,11 +411,11 @@ __global__ __launch_bounds__(kBlock) void cell_mat_kernel(const void* __restrict
   const uint32_t tap_b = C * ES;
   const uint32_t row_b = G * kS * tap_b;
   const uint32_t P = gridDim.x;
-  const uint32_t step_x = (P / G) * kS * row_b;
+  CellStride stride(P, cell, G, tap_b, row_b);
   const uint32_t step_z = P * tap_b;
   uint32_t xo = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES) + (tap0 / kS) * row_b;
   uint32_t zo = (cell * C + c0) * ES;
-  for (; cell < ncells; cell += P, xo += step_x, zo += step_z) {
+  for (; cell < ncells; cell += P, xo += stride.advance(), zo += step_z) {
     Raw<DT, CPT> xr[TPT];
     Raw<DT, CPT> dr[LMAX];
     if constexpr (HAS_BASE) {
@@ -436,7 +466,7 @@ __global__ __launch_bounds__(kBlock) void cell_mat_kernel(const void* __restrict
 // block into LDS as [layer][tap quad][channel] float4 rows, so a wavefront's
 // read of one quad is 64 consecutive 16-byte lanes (no bank conflicts).
 // Block = 4 wavefronts on one 64-channel slab, wavefront w on cell 4 b + w
-// of each grid step (gridDim.x * 4 cells, a multiple of G): each dz run is
+// of each grid step (gridDim.x * 4 cells): each dz run is
 // requested once per cell, where cell_mat_kernel's two tap groups request it
 // twice at these depths.  Same FMA order and roundings as cell_mat_kernel:
 // acc = base, acc = fma(beta_l, dz_l, acc) for l = 0..L-1, one rounding.  When
@@ -478,11 +508,11 @@ __global__ __launch_bounds__(kBlock, 2) void cell_mat_deep_kernel(const void* __
   const uint32_t tap_b = C * ES;
   const uint32_t row_b = G * kS * tap_b;
   const uint32_t P = gridDim.x * 4;
-  const uint32_t step_x = (P / G) * kS * row_b;
+  CellStride stride(P, cell, G, tap_b, row_b);
   const uint32_t step_z = P * tap_b;
   uint32_t xo = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES);
   uint32_t zo = (cell * C + c0) * ES;
-  for (; cell < ncells; cell += P, xo += step_x, zo += step_z) {
+  for (; cell < ncells; cell += P, xo += stride.advance(), zo += step_z) {
     Raw<DT, 1> xr[kK];
     Raw<DT, 1> dr[LMAX];
 #pragma unroll
@@ -793,11 +823,11 @@ __global__ __launch_bounds__(kBlock) void cell_read_multi_kernel(const void* __r
   const uint32_t tap_b = C * ES;
   const uint32_t row_b = G * kS * tap_b;
   const uint32_t P = gridDim.x;
-  const uint32_t step_x = (P / G) * kS * row_b;
+  CellStride stride(P, cell, G, tap_b, row_b);
   const uint32_t step_z = P * tap_b;
   uint32_t go = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES);
   uint32_t zo = (cell * C + c0) * ES;
-  for (; cell < ncells; cell += P, go += step_x, zo += step_z) {
+  for (; cell < ncells; cell += P, go += stride.advance(), zo += step_z) {
     Raw<DT, CPT> gr[kK];
 #pragma unroll
     for (int k = 0; k < kK; ++k) load_at<DT, CPT, true>(g, go + (k / kS) * row_b + (k % kS) * tap_b, gr[k]);
@@ -863,13 +893,13 @@ __global__ __launch_bounds__(kBlock) void cell_wgrad_kernel(const void* __restri
       for (int k = 0; k < TPT; ++k) acc[l][v][k] = 0.f;
   const uint32_t tap_b = C * ES;
   const uint32_t row_b = G * kS * tap_b;
-  const uint32_t P = gridDim.x * WC;  // cell stride, a multiple of G
-  const uint32_t step_x = (P / G) * kS * row_b;
+  const uint32_t P = gridDim.x * WC;  // cell stride
   const uint32_t step_z = P * tap_b;
   uint32_t cell = active ? blockIdx.x * WC + cw : ncells;
+  CellStride stride(P, cell < ncells ? cell : 0, G, tap_b, row_b);
   uint32_t ho = static_cast<uint32_t>((cell_hoff(cell < ncells ? cell : 0, G, C) + c0) * ES) + (tap0 / kS) * row_b;
   uint32_t zo = (cell * C + c0) * ES;
-  for (; cell < ncells; cell += P, ho += step_x, zo += step_z) {
+  for (; cell < ncells; cell += P, ho += stride.advance(), zo += step_z) {
     Raw<DT, CPT> hr[TPT];
     Raw<DT, CPT> dr[LMAX];
 #pragma unroll
@@ -1377,6 +1407,16 @@ int64_t grid_step_cells(int64_t want, int64_t ncells, int G, int cpi) {
   return std::max<int64_t>(unit, std::min<int64_t>(want / unit * unit, cap));
 }
 
+// Cells per grid step of the kernels that step with CellStride (any multiple
+// of `cpi`, the cells per block): `want`, the resident capacity in cells,
+// rounded down to a multiple of cpi, at least cpi and at most ncells rounded
+// up.  Every resident slot is used (rounding the step to a multiple of G left
+// 10 of 170 blocks per slab empty at 256 CUs, two blocks per CU and 3 slabs).
+int64_t grid_cells(int64_t want, int64_t ncells, int cpi) {
+  const int64_t cap = (ncells + cpi - 1) / cpi * cpi;
+  return std::max<int64_t>(cpi, std::min<int64_t>(want / cpi * cpi, cap));
+}
+
 // Shape of the whole-cell kernels per depth bucket: channels per thread CPT
 // and groups per block GR (tap groups of the materialise / weight gradient,
 // layer groups of the multi-weight read).  The LMAX x CPT x 16 / GR fp32
@@ -1491,13 +1531,11 @@ void wgrad_shape(int L, int& tpt, int& cpt);
 template <int DT, int LMAX>
 void cell_wgrad_plan_l(WgradPlan& p, int64_t ncells, int G, int64_t C) {
   constexpr int CPT = CellMatShape<DT, LMAX>::CPT, GR = CellMatShape<DT, LMAX>::GR;
-  constexpr int WC = 4 / GR;  // cell lanes per block: the cell stride nbx * WC must be a multiple of G
+  constexpr int WC = 4 / GR;  // cell lanes per block (the cell stride is nbx * WC)
   static const int per_cu = resident_blocks(cell_wgrad_kernel<DT, LMAX, CPT, GR>);
   p.slabs = static_cast<int>((C / CPT + 63) / 64);
-  const int64_t unit = G / std::gcd<int64_t>(G, WC);
   const int64_t want = static_cast<int64_t>(num_cus()) * per_cu / p.slabs;
-  const int64_t cap = ((ncells + WC - 1) / WC + unit - 1) / unit * unit;
-  p.nbx = std::max<int64_t>(unit, std::min<int64_t>(want / unit * unit, cap));
+  p.nbx = std::max<int64_t>(1, std::min<int64_t>(want, (ncells + WC - 1) / WC));
 }
 
 WgradPlan wgrad_plan(int dt, int64_t ncells, int G, int64_t C, int L, int blocks_per_cu = 2) {
@@ -1606,7 +1644,7 @@ void launch_cell_mat(const void* base, const PtrPack& dz, const PtrPack& beta, v
   const auto kernel = cell_mat_kernel<DT, WDT, LMAX, CPT, GR, HAS_BASE, EXACT>;
   static const int per_cu = resident_blocks(kernel);
   const int slabs = (C / CPT + kBlock / GR - 1) / (kBlock / GR);
-  const int64_t per = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu / slabs, ncells, G, 1);
+  const int64_t per = grid_cells(static_cast<int64_t>(num_cus()) * per_cu / slabs, ncells, 1);
   kernel<<<dim3(static_cast<unsigned>(per), slabs), kBlock, 0, st>>>(base, dz, beta, out, L,
                                                                     static_cast<uint32_t>(ncells), G, C);
 }
@@ -1622,7 +1660,7 @@ void launch_cell_mat_deep(const void* base, const PtrPack& dz, const PtrPack& be
   const auto kernel = cell_mat_deep_kernel<DT, WDT, LMAX, LV, EXACT>;
   static const int per_cu = resident_blocks(kernel);
   const int slabs = (C + 63) / 64;
-  const int64_t per = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu * 4 / slabs, ncells, G, 4);
+  const int64_t per = grid_cells(static_cast<int64_t>(num_cus()) * per_cu * 4 / slabs, ncells, 4);
   PtrPack dp = dz, bp = beta;  // padding layers: layer 0's rows (contributing a selected 0)
   for (int l = L; l < LMAX; ++l) {
     dp.p[l] = dz.p[0];
@@ -1747,7 +1785,7 @@ void launch_cell_read_multi(const void* g, const PtrPack& w, const PtrPack& out,
                                 : cell_read_multi_kernel<DT, WDT, LMAX, CPT, GR, false>;
   static const int per_cu = resident_blocks(cell_read_multi_kernel<DT, WDT, LMAX, CPT, GR, false>);
   const int slabs = (C / CPT + kBlock / GR - 1) / (kBlock / GR);
-  const int64_t per = grid_step_cells(static_cast<int64_t>(num_cus()) * per_cu / slabs, ncells, G, 1);
+  const int64_t per = grid_cells(static_cast<int64_t>(num_cus()) * per_cu / slabs, ncells, 1);
   kernel<<<dim3(static_cast<unsigned>(per), slabs), kBlock, 0, st>>>(g, w, out, L, static_cast<uint32_t>(ncells), G, C);
 }
 
