@@ -35,7 +35,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 METRIC = "read/write/materialise HBM GB/s (% of 8 TB/s) at B=256 C=768 bf16; fwd img/s"
 PEAK_HBM = 8.0e12
 PMC_PROFILE = os.path.join(ROOT, "profiles", "materialise_fwd_b256_pmc.txt")
-KERNEL_SOURCE = os.path.join(ROOT, "flowmatching_lthc_amd", "csrc", "lthc_kernels.hip")
+KERNEL_SOURCES = os.path.join(ROOT, "flowmatching_lthc_amd", "csrc")
+KERNEL_HEADER = os.path.join(ROOT, "include", "lthc.h")
 
 
 def parse_args():
@@ -82,10 +83,17 @@ def algorithmic_bytes(B, G, C, L, e=2):
 
 
 def kernel_source_sha1():
-    """sha1 of the source file that holds the materialise kernel (the PMC summary records the one it measured)."""
+    """sha1 over every source the library is compiled from: lthc_kernels.hip, the .inc files it includes (in name
+    order, each preceded by its name) and include/lthc.h.  The PMC summaries record the one they measured."""
     import hashlib
 
-    return hashlib.sha1(open(KERNEL_SOURCE, "rb").read()).hexdigest()
+    h = hashlib.sha1()
+    names = sorted(n for n in os.listdir(KERNEL_SOURCES) if n.endswith((".hip", ".inc")))
+    for path in [os.path.join(KERNEL_SOURCES, n) for n in names] + [KERNEL_HEADER]:
+        h.update(os.path.basename(path).encode() + b"\0")
+        with open(path, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
 
 
 def pmc_traffic():

@@ -652,6 +652,7 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
             and t2.dtype == x.dtype
             and isinstance(fl.norm_final, RMSNorm)
             and fl.linear.bias is not None
+            and self.patch_size == 4
             and ops.decoder_head_supported(x, fl.linear.weight)
         ):
             # RMSNorm + modulate + linear + unpatchify in one pass (jit_thc::decoder_head): y never reaches memory
@@ -674,10 +675,14 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
             and isinstance(fl.norm_final, RMSNorm)
             and fl.linear.bias is not None
             and "final_accumulate_reference" not in self.__dict__
-            and type(self).final_accumulate_reference
-            in (
-                SharedReadLocalTHCSharedAdaLNJiT.final_accumulate_reference,
-                SharedReadFusedFinal12LocalTHCSharedAdaLNJiT.final_accumulate_reference,
+            and (
+                type(self).final_accumulate_reference is SharedReadLocalTHCSharedAdaLNJiT.final_accumulate_reference
+                # the fused-final-12 hook takes exactly 12 layers: other depths reach its ValueError below
+                or (
+                    type(self).final_accumulate_reference
+                    is SharedReadFusedFinal12LocalTHCSharedAdaLNJiT.final_accumulate_reference
+                    and len(dz_list) == 12
+                )
             )
             and len(dz_list) == len(self.blocks)
             and t2.dtype == x0.dtype

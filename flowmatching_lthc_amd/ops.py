@@ -1231,8 +1231,8 @@ def decoder_head(
             f"lin_weight [{DECODER_OUTPUTS}, C]; got {tuple(x.shape)} {x.dtype}, {tuple(lin_weight.shape)}"
         )
     b, t, c = x.shape
-    if h <= 0 or t % h != 0 or patch <= 0 or DECODER_OUTPUTS % (patch * patch) != 0:
-        raise ValueError(f"token grid {h} x {t // max(h, 1)} and patch {patch} do not fit {t} tokens, 48 outputs")
+    if h <= 0 or t % h != 0 or patch != 4:
+        raise ValueError(f"token grid {h} x {t // max(h, 1)} and patch {patch}: {t} tokens and 4 x 4 patches expected")
     w = t // h
     co = DECODER_OUTPUTS // (patch * patch)
     for name, v in (("shift", shift), ("scale", scale)):
@@ -1261,7 +1261,7 @@ def decoder_head(
 
 def materialise_decoder_supported(x0: Tensor, dzs: Sequence[Tensor], lin_weight: Tensor, patch: int) -> bool:
     """Whether jit_thc::final_accumulate_decoder_head takes these operands: bf16 / fp16 x0 [B, 4G, 4G, C] with
-    G % 16 == 0, C % 256 == 0, 1..12 layers, 48 outputs per token, below 4 GiB."""
+    G % 16 == 0, C % 256 == 0, 1..12 layers, 4 x 4 patches of 3 channels (48 outputs per token), below 4 GiB."""
     if not (x0.is_cuda and x0.dim() == 4 and x0.dtype in (torch.bfloat16, torch.float16)):
         return False
     b, h, w, c = x0.shape
@@ -1270,8 +1270,7 @@ def materialise_decoder_supported(x0: Tensor, dzs: Sequence[Tensor], lin_weight:
         and h % (4 * 16) == 0
         and c % 256 == 0
         and 1 <= len(dzs) <= 12
-        and patch > 0
-        and DECODER_OUTPUTS % (patch * patch) == 0
+        and patch == 4
         and tuple(lin_weight.shape) == (DECODER_OUTPUTS, c)
         and x0.numel() * 2 < 2**32
     )
@@ -1292,8 +1291,9 @@ def final_accumulate_decoder_head(
     _check_list(x0, dzs, betas)
     if not materialise_decoder_supported(x0, dzs, lin_weight, patch):
         raise ValueError(
-            f"x0 must be bf16 or fp16 [B, 4G, 4G, C] with G % 16 == 0, C % 256 == 0, 1..12 layers and lin_weight "
-            f"[{DECODER_OUTPUTS}, C]; got {tuple(x0.shape)} {x0.dtype}, {len(dzs)} layers, {tuple(lin_weight.shape)}"
+            f"x0 must be bf16 or fp16 [B, 4G, 4G, C] with G % 16 == 0, C % 256 == 0, 1..12 layers, lin_weight "
+            f"[{DECODER_OUTPUTS}, C] and patch 4; got {tuple(x0.shape)} {x0.dtype}, {len(dzs)} layers, "
+            f"{tuple(lin_weight.shape)}, patch {patch}"
         )
     b, h, _, c = x0.shape
     g = h // S

@@ -137,7 +137,7 @@ int lthc_weight_grad(const void* high, const void* const* low, int x_dtype, floa
  * lthc_read_multi_fwd(G, beta) and lthc_weight_grad(G, dz), but G (the
  * largest tensor) is read once instead of twice.  gdz is bitwise equal to
  * lthc_read_multi_fwd's.  One LDS-staged tile kernel for 16-bit activations
- * with L <= 24, C % 64 == 0, G % 8 == 0 and 16-byte aligned dz; otherwise one
+ * with L <= 24, C % 64 == 0, G % 8 == 0 and 16-byte aligned dz and gdz; otherwise one
  * register kernel when L <= 24, C % 64 == 0 and G is below 4 GiB; otherwise
  * the two separate passes.  `dz`, `beta`, `gdz` are host arrays of L device
  * pointers; the workspace holds the fp32 partials.
@@ -156,7 +156,10 @@ int lthc_materialise_bwd(const void* g, int x_dtype, const void* const* dz, cons
  * calls no allocator.  Shapes whose partials need more than the scratch array
  * (lthc_materialise_bwd_workspace_bytes() > 64 MiB) return LTHC_ERR_UNSUPPORTED.
  * All calls on one GPU share the array, which keeps the last call's contents:
- * calls that overlap on one GPU race; the caller serialises them.
+ * calls that overlap on one GPU race; the caller serialises them.  The first
+ * call on a device looks up that device's scratch address and the launch
+ * plans (occupancy queries): make it outside graph capture; later calls may be
+ * captured and replayed.
  */
 size_t lthc_noalloc_scratch_bytes(void);
 int lthc_materialise_bwd_noalloc(const void* g, int x_dtype, const void* const* dz, const void* const* beta,
@@ -338,8 +341,8 @@ int lthc_qk_norm_rope_attention(const void* qkv, int x_dtype, const void* q_weig
  * fp32 (matrix cores); W and bias are rounded to x_dtype first, as autocast
  * casts them.  norm_weight [C], lin_weight [48, C] and lin_bias [48] are fp32
  * or x_dtype; shift / scale rows [B, C] at row stride mod_ld, x_dtype.
- * C a multiple of 32 up to 768; h*w a multiple of 64; x and lin_weight
- * 16-byte aligned.
+ * C a multiple of 32 up to 768; h*w a multiple of 64; P == 4 and CO == 3;
+ * x and lin_weight 16-byte aligned.
  */
 int lthc_decoder_fwd(const void* x, int x_dtype, const void* norm_weight, int nw_dtype, const void* shift,
                      const void* scale, int64_t mod_ld, const void* lin_weight, int lw_dtype, const void* lin_bias,
@@ -362,7 +365,7 @@ int lthc_decoder_fwd(const void* x, int x_dtype, const void* norm_weight, int nw
  * function, not bit for bit).  x_dtype bf16 or fp16; beta fp32 [C,16]
  * (16-byte aligned); norm_weight, lin_weight [48, C], lin_bias fp32 or
  * x_dtype; shift / scale rows [B, C] at row stride mod_ld, x_dtype.  s == 4,
- * C % 256 == 0, G % 16 == 0, L <= 12, P*P*CO == 48, x0 below 4 GiB, img
+ * C % 256 == 0, G % 16 == 0, L <= 12, P == 4 and CO == 3, x0 below 4 GiB, img
  * 16-byte aligned.  The caller workspace (256-byte aligned) holds M_b, Q_b's
  * partial sums and the per-slab fp32 partial rows (3 KiB per cell and 256
  * channels).
@@ -474,7 +477,7 @@ int lthc_read_bwd(const void* gz, const void* x, int x_dtype, const void* alpha,
  * z[0..L] and x_out, bitwise the per-op entry points' values), and otherwise
  * composes them (read, gamma, recurrence prefix, materialise).  The backward is one pass over gx and the dz and gz
  * stacks for 16-bit activations with L <= 24, C % 64 == 0, G % 8 == 0 and
- * 16-byte aligned gx, dx0, alpha and x0 (one tile kernel forms gamma, writes
+ * 16-byte aligned gx, dx0, alpha and dz, gz and ddz entries (one tile kernel forms gamma, writes
  * ddz, dx0 and S_0 and the partial sums of dbeta and of the gamma terms; then
  * dalpha's pass over x0 and S_0 and one launch of the reductions), and otherwise a composition (materialise backward; the
  * recurrence steps in one pass over H, dZ and gdZ up to depth 24, one

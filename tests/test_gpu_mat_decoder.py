@@ -148,3 +148,26 @@ def test_materialise_decoder_graph_replay_equals_eager():
         other = ops.final_accumulate_decoder_head(x0 * 0.5, dzs, betas, nw, shift, scale, lw, lb, 1e-6, 4)  # eager work
         torch.cuda.synchronize()
         assert not torch.equal(other, eager)
+
+
+def test_fused_final12_other_depth_raises_under_no_grad():
+    """SharedReadFusedFinal12LocalTHCSharedAdaLNJiT requires depth 12 (local_thc.py:1416-1418).  A model of another
+    depth must raise that ValueError under no-grad too, where the fused materialise + decoder path would otherwise
+    run without calling the hook; the same model class at depth 12 takes the fused path."""
+    print("case FusedFinal12 depth 2", flush=True)
+    kw = dict(input_size=256, patch_size=4, hidden_size=256, num_heads=4, bottleneck_dim=16, workspace_grid=16)
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(1, 3, 256, 256, generator=gen).to(DEV)
+    t = torch.rand(1, generator=gen).to(DEV)
+    y = torch.randint(0, 1000, (1,), generator=gen).to(DEV)
+    for depth, fused_calls in ((2, None), (12, 1)):
+        m = M.SharedReadFusedFinal12LocalTHCSharedAdaLNJiT(depth=depth, **kw).to(DEV).eval()
+        with torch.no_grad(), torch.autocast("cuda", dtype=torch.bfloat16):
+            with mock.patch.object(ops, "final_accumulate_decoder_head", wraps=ops.final_accumulate_decoder_head) as op:
+                if fused_calls is None:
+                    with pytest.raises(ValueError, match="depth=12"):
+                        m(x, t, y)
+                    assert op.call_count == 0
+                else:
+                    m(x, t, y)
+                    assert op.call_count == fused_calls

@@ -16,7 +16,7 @@ import numpy as np
 import pytest
 import torch
 
-from flowmatching_lthc_amd import ops
+from flowmatching_lthc_amd import _abi, ops
 from oracle import oracle as O
 
 from . import capi
@@ -783,8 +783,9 @@ def test_interface_bwd_one_pass_suffix_equals_per_step_chain(xdt, L, missing, G)
 
 
 def test_interface_bwd_unaligned_x0_equals_aligned():
-    """An X0 that is 8- but not 16-byte aligned keeps lthc_interface_bwd off the tile kernel (its 16-byte X0 reads):
-    the composed form then gives the same dZ gradients and dX0 bit for bit, and the weight gradients to 1e-5."""
+    """An X0 that is 8- but not 16-byte aligned: the tile kernel does not read X0 (dalpha's pass reads it with
+    2-byte lanes), so lthc_interface_bwd gives the same dZ gradients and dX0 bit for bit, and the weight gradients
+    to 1e-5."""
     print("case unaligned x0", flush=True)
     B, G, C, L = 2, 16, 256, 5
     d = cfg(B, G, C, L, seed=77, grads=True)
@@ -804,6 +805,63 @@ def test_interface_bwd_unaligned_x0_equals_aligned():
     for g, r, what in ((got[2], ref[2], "dalpha"), (got[3], ref[3], "dbeta")):
         err = ((g - r).abs().max() / r.abs().max()).item()
         assert err <= 1e-5, f"{what}: {err:.3e}"
+
+def _offset_views(ts):
+    """Copies of `ts` whose storage starts 8 bytes past a 16-byte boundary (4-element aligned for 16-bit dtypes)."""
+    out = []
+    for t in ts:
+        buf = torch.empty(t.numel() + 8 // t.element_size(), dtype=t.dtype, device=t.device)
+        v = buf[8 // t.element_size() :].view_as(t)
+        assert v.data_ptr() % 16 == 8
+        out.append(v)
+    return out
+
+
+def test_tile_backward_outputs_8_bytes_off_equal_aligned():
+    """The tile kernel writes gdZ / ddz with 16-byte stores, so outputs that are only 8-byte aligned (the ABI's
+    4-element rule for bf16) must take the other kernels: lthc_materialise_bwd's gdZ and lthc_interface_bwd's ddz
+    and dX0 then equal the aligned calls bit for bit, and the weight gradients agree to 1e-5."""
+    print("case tile outputs 8 bytes off", flush=True)
+    B, G, C, L = 2, 16, 256, 5
+    d = cfg(B, G, C, L, seed=78, grads=True)
+    x0, alpha = dev(d["x0"], BF16), dev(d["alpha"])
+    betas, dzs = [dev(b) for b in d["beta"]], [dev(z, BF16) for z in d["dz"]]
+    gx, gzs = dev(d["grad_xl"], BF16), [dev(g, BF16) for g in d["grad_z"]]
+    lib, st = _abi.load(), torch.cuda.current_stream().cuda_stream
+    # materialise backward
+    ref_dz, ref_gb = capi.materialise_bwd(gx, dzs, betas)
+    gdz = _offset_views(dzs)
+    gb = torch.empty((L, C, 16), device=DEV)
+    ws = torch.empty((int(lib.lthc_materialise_bwd_workspace_bytes(B, G, 4, C, L)) + 16,), device=DEV, dtype=torch.uint8)
+    rc = lib.lthc_materialise_bwd(
+        gx.data_ptr(), _abi.BF16, _abi.ptr_array(dzs), _abi.ptr_array(betas), _abi.F32, _abi.ptr_array(gdz),
+        gb.data_ptr(), B, G, 4, C, L, ws.data_ptr(), ws.numel(), st,
+    )  # fmt: skip
+    _abi.check(rc, "lthc_materialise_bwd")
+    for l in range(L):
+        assert torch.equal(gdz[l], ref_dz[l]), f"gdZ_{l}"
+    assert ((gb - ref_gb).abs().max() / ref_gb.abs().max()).item() <= 1e-5
+    # whole-interface backward
+    ref = capi.interface_bwd(gx, gzs, x0, dzs, alpha, betas)
+    ddz = _offset_views(dzs)
+    dx0 = torch.empty_like(x0)
+    da = torch.empty((C, 16), device=DEV)
+    db = torch.empty((L, C, 16), device=DEV)
+    ws = torch.empty((int(lib.lthc_interface_workspace_bytes(B, G, 4, C, L)) + 16,), device=DEV, dtype=torch.uint8)
+    rc = lib.lthc_interface_bwd(
+        gx.data_ptr(), _abi.ptr_array(gzs), _abi.BF16, x0.data_ptr(), _abi.ptr_array(dzs), alpha.data_ptr(),
+        _abi.ptr_array(betas), _abi.F32, dx0.data_ptr(), _abi.ptr_array(ddz), da.data_ptr(), db.data_ptr(),
+        B, G, 4, C, L, ws.data_ptr(), ws.numel(), st,
+    )  # fmt: skip
+    _abi.check(rc, "lthc_interface_bwd")
+    torch.cuda.synchronize()
+    assert torch.equal(dx0, ref[0]), "dX0"
+    for l in range(L):
+        assert torch.equal(ddz[l], ref[1][l]), f"ddZ_{l}"
+    for g, r, what in ((da, ref[2], "dalpha"), (db, ref[3], "dbeta")):
+        err = ((g - r).abs().max() / r.abs().max()).item()
+        assert err <= 1e-5, f"{what}: {err:.3e}"
+
 
 def test_interface_entry_points_bf16_configuration3_slice(coracle):
     """The whole-interface entry points at configuration 3's width and depth (B=4 slice, bf16, fp32 weights):
