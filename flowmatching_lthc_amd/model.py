@@ -114,6 +114,8 @@ class VisionRotaryEmbeddingFast(nn.Module):
         buffers change (a new device or dtype, or an in-place update)."""
         if self.freqs_cos.dtype == dtype:
             return self.freqs_cos, self.freqs_sin
+        if torch.compiler.is_compiling():  # the compiled graph holds the conversion (no cache keyed on addresses)
+            return self.freqs_cos.to(dtype), self.freqs_sin.to(dtype)
         key = (dtype, self.freqs_cos.data_ptr(), self.freqs_cos._version, self.freqs_sin.data_ptr(), self.freqs_sin._version)
         cache = self.__dict__.get("_cast_tables")
         if cache is None or cache[0] != key:
@@ -725,21 +727,26 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
         """Inference on the GPU with the standard blocks, hooks, branch and ungrouped weights: jit_thc::block_tail
         applies."""
         std = SharedReadLocalTHCSharedAdaLNJiTBlock
-        return (
+        if not (
             self.fused_block_tail
             and not torch.is_grad_enabled()
             and z.is_cuda
             and len(self.blocks) > 1
             and self.shared_read.group_dim == 1
-            and all(
+        ):
+            return False
+        for blk in self.blocks:  # a plain loop (torch.compile traces it without a graph break)
+            if not (
                 blk.write.group_dim == 1
                 and type(blk) is std
-                and not {"branch_update", "lazy_workspace_step", "lazy_workspace_update"} & blk.__dict__.keys()
+                and "branch_update" not in blk.__dict__
+                and "lazy_workspace_step" not in blk.__dict__
+                and "lazy_workspace_update" not in blk.__dict__
                 and type(blk.branch) is WorkspaceSharedAdaLNBranch
                 and "forward" not in blk.branch.__dict__
-                for blk in self.blocks
-            )
-        )
+            ):
+                return False
+        return True
 
     def _blocks_fused_tail(self, z: torch.Tensor, t6: torch.Tensor) -> list[torch.Tensor] | None:
         """The block loop of forward_lazy with each block's gate_residual, its recurrence step and the next block's
@@ -772,16 +779,18 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
         same dtype sequence), or None where it does not apply (CPU, grouped write weights, another block type)."""
         writes = [blk.write for blk in self.blocks]
         std = SharedReadLocalTHCSharedAdaLNJiTBlock
-        own_hooks = not overridden(self.shared_read, "alpha", SharedLocalRead) and all(
-            # no block replaces a hook the gammas come from (subclass or instance override)
-            not overridden(blk, "lazy_workspace_step", std)
-            and not overridden(blk, "lazy_workspace_update", std)
-            and not overridden(blk.write, "gamma_from_alpha", LayerLocalWrite)
-            and not overridden(blk.write, "beta", LayerLocalWrite)
-            for blk in self.blocks
-        )
-        if not dz.is_cuda or not own_hooks or self.shared_read.group_dim != 1 or any(w.group_dim != 1 for w in writes):
+        if not dz.is_cuda or overridden(self.shared_read, "alpha", SharedLocalRead) or self.shared_read.group_dim != 1:
             return None
+        for blk in self.blocks:  # a plain loop (torch.compile traces it without a graph break)
+            # no block replaces a hook the gammas come from (subclass or instance override)
+            if (
+                overridden(blk, "lazy_workspace_step", std)
+                or overridden(blk, "lazy_workspace_update", std)
+                or overridden(blk.write, "gamma_from_alpha", LayerLocalWrite)
+                or overridden(blk.write, "beta", LayerLocalWrite)
+                or blk.write.group_dim != 1
+            ):
+                return None
         return list(ops.lazy_gamma_rounded(self.shared_read.alpha(), [w.write_weight for w in writes], dz.dtype).unbind(0))
 
     def forward_naive(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
@@ -793,6 +802,10 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
 
     def forward(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor, use_lazy: bool | None = None) -> torch.Tensor:
         lazy = self.use_lazy if use_lazy is None else use_lazy
+        if torch.compiler.is_compiling():
+            # under torch.compile the compiler fuses autocast's weight conversions itself; the one-launch table
+            # (built eagerly, kept on the module) is for eager and HIP-graph forwards
+            return self.forward_lazy(x, t, y) if lazy else self.forward_naive(x, t, y)
         with self._converted_weights():
             return self.forward_lazy(x, t, y) if lazy else self.forward_naive(x, t, y)
 

@@ -23,8 +23,10 @@ Naming follows the reference: the legacy "write" op is the algorithmic READ
 
 from __future__ import annotations
 
+import functools
 import math
-from typing import Sequence
+import sys
+from typing import Callable, Sequence
 
 import torch
 from torch import Tensor
@@ -33,6 +35,57 @@ from . import _abi
 
 S = 4  # cell side (taps K = 16)
 K = S * S
+
+
+# ---------------------------------------------------------------------------
+# torch.compile: every jit_thc op is an opaque Inductor fallback
+# ---------------------------------------------------------------------------
+_inductor_fallbacks_done = False
+
+
+def _register_inductor_fallbacks() -> None:
+    """Registers every jit_thc op as an Inductor fallback kernel, with the layout constraint its tags give (the
+    default: fixed stride order), which is what Inductor does by itself the first time it lowers an op it has no
+    lowering for.  Done ahead of time because Inductor's own path formats the op's arguments for a log message
+    whatever the log level, and those arguments print their whole producer graph: for the 25-argument
+    materialisation, whose dz arguments end chains of twelve blocks of fallback ops, that text grows exponentially
+    with the depth and held a compile of the LTHC-B/4 model for many minutes.  Runs once, from the first fake-tensor
+    evaluation of a jit_thc op after Inductor's lowering module has been imported (AOTAutograd traces the graph with
+    fake tensors after that import and before any lowering); before that, nothing is imported here."""
+    global _inductor_fallbacks_done
+    if _inductor_fallbacks_done or "torch._inductor.lowering" not in sys.modules:
+        return
+    _inductor_fallbacks_done = True
+    from torch._inductor.lowering import lowerings, make_fallback, tag_to_layout_constraint
+    from torch._library.utils import get_layout_constraint_tag
+
+    for name in dir(torch.ops.jit_thc):
+        packet = getattr(torch.ops.jit_thc, name)
+        if not isinstance(packet, torch._ops.OpOverloadPacket):
+            continue
+        for overload in packet.overloads():
+            op = getattr(packet, overload)
+            if op not in lowerings:
+                make_fallback(op, layout_constraint=tag_to_layout_constraint(get_layout_constraint_tag(op, with_default=True)))
+
+
+def _fake(op) -> Callable:
+    """Decorator registering `fn` as the fake (meta) implementation of `op` (a custom op, or a "jit_thc::name"
+    string for ops defined with torch.library.define), registering the Inductor fallbacks first."""
+
+    def deco(fn: Callable) -> Callable:
+        @functools.wraps(fn)
+        def fake(*args, **kwargs):
+            _register_inductor_fallbacks()
+            return fn(*args, **kwargs)
+
+        if isinstance(op, str):
+            torch.library.register_fake(op)(fake)
+        else:
+            op.register_fake(fake)
+        return fake
+
+    return deco
 
 
 # ---------------------------------------------------------------------------
@@ -202,7 +255,7 @@ def final_accumulate_backward(grad_out: Tensor, dzs: list[Tensor], betas: list[T
     return gdz, gb
 
 
-@final_accumulate_backward.register_fake
+@_fake(final_accumulate_backward)
 def _(grad_out: Tensor, dzs: list[Tensor], betas: list[Tensor]):
     b, g, c = _hi_geom(grad_out, "grad_out")
     return grad_out.new_empty((len(dzs), b, g * g, c)), grad_out.new_empty((len(dzs), c, K), dtype=torch.float32)
@@ -224,7 +277,7 @@ def local_write_traceable(x: Tensor, weight: Tensor) -> Tensor:
     return z
 
 
-@local_write_traceable.register_fake
+@_fake(local_write_traceable)
 def _(x: Tensor, weight: Tensor) -> Tensor:
     b, g, c = _hi_geom(x)
     return x.new_empty((b, g * g, c))
@@ -246,7 +299,7 @@ def local_read_traceable(z: Tensor, weight: Tensor) -> Tensor:
     return out
 
 
-@local_read_traceable.register_fake
+@_fake(local_read_traceable)
 def _(z: Tensor, weight: Tensor) -> Tensor:
     b, g, c = _lo_geom(z)
     return z.new_empty((b, g * S, g * S, c))
@@ -268,7 +321,7 @@ def local_weight_grad_traceable(high: Tensor, low: Tensor) -> Tensor:
     return _launch_weight_grad(high, [low])[0]
 
 
-@local_weight_grad_traceable.register_fake
+@_fake(local_weight_grad_traceable)
 def _(high: Tensor, low: Tensor) -> Tensor:
     c = high.shape[3]
     return high.new_empty((c, K), dtype=torch.float32)
@@ -324,7 +377,7 @@ def local_read_add_traceable(z: Tensor, weight: Tensor, x: Tensor) -> Tensor:
     return out
 
 
-@local_read_add_traceable.register_fake
+@_fake(local_read_add_traceable)
 def _(z: Tensor, weight: Tensor, x: Tensor) -> Tensor:
     return torch.empty_like(x)
 
@@ -474,7 +527,7 @@ def final_accumulate_b4_traceable(x0: Tensor, dz_stack: Tensor, beta_stack: Tens
     return out
 
 
-@final_accumulate_b4_traceable.register_fake
+@_fake(final_accumulate_b4_traceable)
 def _(x0: Tensor, dz_stack: Tensor, beta_stack: Tensor) -> Tensor:
     return torch.empty_like(x0)
 
@@ -494,7 +547,7 @@ def final_accumulate_b4_grad_dz_traceable(grad_out: Tensor, beta_stack: Tensor) 
     return gdz
 
 
-@final_accumulate_b4_grad_dz_traceable.register_fake
+@_fake(final_accumulate_b4_grad_dz_traceable)
 def _(grad_out: Tensor, beta_stack: Tensor) -> Tensor:
     b, g, c = _hi_geom(grad_out, "grad_out")
     return grad_out.new_empty((beta_stack.shape[0], b, g * g, c))
@@ -510,7 +563,7 @@ def final_accumulate_b4_grad_beta_traceable(grad_out: Tensor, dz_stack: Tensor, 
     return _launch_weight_grad(grad_out, list(dz_stack.unbind(0)))
 
 
-@final_accumulate_b4_grad_beta_traceable.register_fake
+@_fake(final_accumulate_b4_grad_beta_traceable)
 def _(grad_out: Tensor, dz_stack: Tensor, beta_stack: Tensor) -> Tensor:
     return grad_out.new_empty((dz_stack.shape[0], grad_out.shape[3], K), dtype=torch.float32)
 
@@ -571,7 +624,7 @@ def final_accumulate_list(x0: Tensor, dzs: list[Tensor], betas: list[Tensor]) ->
     return out
 
 
-@final_accumulate_list.register_fake
+@_fake(final_accumulate_list)
 def _(x0: Tensor, dzs: list[Tensor], betas: list[Tensor]) -> Tensor:
     return torch.empty_like(x0)
 
@@ -592,7 +645,7 @@ def final_accumulate_list_grad_dz(grad_out: Tensor, betas: list[Tensor]) -> list
     return outs
 
 
-@final_accumulate_list_grad_dz.register_fake
+@_fake(final_accumulate_list_grad_dz)
 def _(grad_out: Tensor, betas: list[Tensor]) -> list[Tensor]:
     b, g, c = _hi_geom(grad_out, "grad_out")
     return [grad_out.new_empty((b, g * g, c)) for _ in betas]
@@ -611,7 +664,7 @@ def final_accumulate_list_grad_beta(grad_out: Tensor, dzs: list[Tensor]) -> Tens
     return _launch_weight_grad(grad_out, dzs)
 
 
-@final_accumulate_list_grad_beta.register_fake
+@_fake(final_accumulate_list_grad_beta)
 def _(grad_out: Tensor, dzs: list[Tensor]) -> Tensor:
     return grad_out.new_empty((len(dzs), grad_out.shape[3], K), dtype=torch.float32)
 
@@ -678,7 +731,7 @@ def final_accumulate_b4_12_traceable(
     return out
 
 
-@final_accumulate_b4_12_traceable.register_fake
+@_fake(final_accumulate_b4_12_traceable)
 def _(x0, *rest):
     return torch.empty_like(x0)
 
@@ -704,7 +757,7 @@ def final_accumulate_b4_12_grad_dz_ptr_traceable(
     return gdz
 
 
-@final_accumulate_b4_12_grad_dz_ptr_traceable.register_fake
+@_fake(final_accumulate_b4_12_grad_dz_ptr_traceable)
 def _(grad_out, *betas):
     b, g, c = _hi_geom(grad_out, "grad_out")
     return grad_out.new_empty((12, b, g * g, c))
@@ -728,7 +781,7 @@ def final_accumulate_b4_12_grad_beta_ptr_traceable(
     return _launch_weight_grad(grad_out, dzs)
 
 
-@final_accumulate_b4_12_grad_beta_ptr_traceable.register_fake
+@_fake(final_accumulate_b4_12_grad_beta_ptr_traceable)
 def _(grad_out, *dzs):
     return grad_out.new_empty((12, grad_out.shape[3], K), dtype=torch.float32)
 
@@ -794,7 +847,7 @@ def lazy_workspace_update(z: Tensor, dz: Tensor, gamma: Tensor) -> Tensor:
     return out
 
 
-@lazy_workspace_update.register_fake
+@_fake(lazy_workspace_update)
 def _(z: Tensor, dz: Tensor, gamma: Tensor) -> Tensor:
     return z.new_empty(z.shape, dtype=torch.promote_types(z.dtype, dz.dtype))
 
@@ -826,7 +879,7 @@ def lazy_workspace_update_backward(
     return gdz, ggamma
 
 
-@lazy_workspace_update_backward.register_fake
+@_fake(lazy_workspace_update_backward)
 def _(grad: Tensor, dz: Tensor, gamma: Tensor, gdz_add: Tensor | None = None):
     return torch.empty_like(grad), grad.new_empty((grad.shape[-1],), dtype=torch.float32)
 
@@ -864,7 +917,7 @@ def lazy_workspace_update_backward_sum(
     return gsum, gdz, ggamma
 
 
-@lazy_workspace_update_backward_sum.register_fake
+@_fake(lazy_workspace_update_backward_sum)
 def _(grad: Tensor, grad_branch: Tensor, dz: Tensor, gamma: Tensor, gdz_add: Tensor | None = None):
     return torch.empty_like(grad), torch.empty_like(grad), grad.new_empty((grad.shape[-1],), dtype=gamma.dtype)
 
@@ -971,7 +1024,7 @@ def lazy_gamma_stack(alpha: Tensor, beta_stack: Tensor) -> Tensor:
     return out
 
 
-@lazy_gamma_stack.register_fake
+@_fake(lazy_gamma_stack)
 def _(alpha: Tensor, beta_stack: Tensor) -> Tensor:
     return alpha.new_empty((beta_stack.shape[0], alpha.shape[0]), dtype=torch.float32)
 
@@ -1024,7 +1077,7 @@ def lazy_gamma_rounded(alpha: Tensor, betas: list[Tensor], dtype: torch.dtype) -
     return out
 
 
-@lazy_gamma_rounded.register_fake
+@_fake(lazy_gamma_rounded)
 def _(alpha: Tensor, betas: list[Tensor], dtype: torch.dtype) -> Tensor:
     return alpha.new_empty((len(betas), alpha.shape[0]), dtype=dtype)
 
@@ -1035,18 +1088,20 @@ def _setup_gamma_rounded_ctx(ctx, inputs, output):
     ctx.dtype = dtype
 
 
-def _backward_gamma_rounded(ctx, grad):
-    """Eager autograd's values for lazy_gamma_rounded_eager, from one lthc_gamma_rounded_bwd launch."""
-    alpha, *betas = ctx.saved_tensors
-    need_a, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
-    if not (need_a or need_b):
-        return None, None, None
+@torch.library.custom_op("jit_thc::lazy_gamma_rounded_backward", mutates_args=())
+def lazy_gamma_rounded_backward(
+    grad: Tensor, alpha: Tensor, betas: list[Tensor], need_alpha: bool, need_beta: bool
+) -> tuple[Tensor, list[Tensor]]:
+    """Eager autograd's values for lazy_gamma_rounded_eager from one lthc_gamma_rounded_bwd launch: (grad of
+    alpha, or an empty tensor when not needed; grads of the betas in the first beta's dtype, or an empty list).
+    An op of its own so that the backward is opaque to torch.compile's tracing."""
+    _on_gpu(grad, alpha, *betas)
     bd = betas[0].dtype
     betas = [b.contiguous() if b.dtype == bd else b.to(bd).contiguous() for b in betas]
     alpha = alpha.contiguous()
-    grad = grad.to(ctx.dtype).contiguous()
-    ga = torch.empty_like(alpha) if need_a else None
-    gbs = [torch.empty_like(b) for b in betas] if need_b else None
+    grad = grad.contiguous()
+    ga = torch.empty_like(alpha) if need_alpha else None
+    gbs = [torch.empty_like(b) for b in betas] if need_beta else None
     c, k = alpha.shape
     with _on_device(alpha):
         rc = _abi.load().lthc_gamma_rounded_bwd(
@@ -1055,9 +1110,25 @@ def _backward_gamma_rounded(ctx, grad):
             _abi.stream_of(alpha),
         )  # fmt: skip
     _abi.check(rc, "lthc_gamma_rounded_bwd")
-    if gbs is not None:
-        gbs = [g if g.dtype == b.dtype else g.to(b.dtype) for g, b in zip(gbs, ctx.saved_tensors[1:])]
-    return ga, gbs, None
+    return (ga if ga is not None else alpha.new_empty((0,))), (gbs if gbs is not None else [])
+
+
+@_fake(lazy_gamma_rounded_backward)
+def _(grad: Tensor, alpha: Tensor, betas: list[Tensor], need_alpha: bool, need_beta: bool):
+    ga = alpha.new_empty(alpha.shape) if need_alpha else alpha.new_empty((0,))
+    gbs = [betas[0].new_empty(b.shape) for b in betas] if need_beta else []
+    return ga, gbs
+
+
+def _backward_gamma_rounded(ctx, grad):
+    """Eager autograd's values for lazy_gamma_rounded_eager, from one lthc_gamma_rounded_bwd launch."""
+    alpha, *betas = ctx.saved_tensors
+    need_a, need_b = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
+    if not (need_a or need_b):
+        return None, None, None
+    ga, gbs = lazy_gamma_rounded_backward(grad.to(ctx.dtype), alpha, betas, bool(need_a), bool(need_b))
+    gbs = [g if g.dtype == b.dtype else g.to(b.dtype) for g, b in zip(gbs, betas)] if need_b else None
+    return (ga if need_a else None), gbs, None
 
 
 torch.library.register_autograd(lazy_gamma_rounded, _backward_gamma_rounded, setup_context=_setup_gamma_rounded_ctx)
@@ -1126,7 +1197,7 @@ def norm_modulate(x: Tensor, weight: Tensor, shift: Tensor, scale: Tensor, eps: 
     return y, inv
 
 
-@norm_modulate.register_fake
+@_fake(norm_modulate)
 def _(x: Tensor, weight: Tensor, shift: Tensor, scale: Tensor, eps: float):
     return torch.empty_like(x), x.new_empty((x.shape[0] * x.shape[1],), dtype=torch.float32)
 
@@ -1157,7 +1228,7 @@ def norm_modulate_backward(
     return gx, gw, gsh, gsc
 
 
-@norm_modulate_backward.register_fake
+@_fake(norm_modulate_backward)
 def _(grad: Tensor, x: Tensor, weight: Tensor, scale: Tensor, inv: Tensor):
     b, n, c = x.shape
     f32 = torch.float32
@@ -1323,13 +1394,13 @@ def final_accumulate_decoder_head(
     return img
 
 
-@final_accumulate_decoder_head.register_fake
+@_fake(final_accumulate_decoder_head)
 def _(x0, dzs, betas, norm_weight, shift, scale, lin_weight, lin_bias, eps, patch):
     b, h, _, _ = x0.shape
     return x0.new_empty((b, DECODER_OUTPUTS // (patch * patch), h * patch, h * patch))
 
 
-@decoder_head.register_fake
+@_fake(decoder_head)
 def _(x, norm_weight, shift, scale, lin_weight, lin_bias, eps, h, patch):
     b, t, _ = x.shape
     co = DECODER_OUTPUTS // (patch * patch)

@@ -37,7 +37,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from . import _abi
-from .ops import _mod_rows, _norm_weight, _on_device, _on_gpu
+from .ops import _fake, _mod_rows, _norm_weight, _on_device, _on_gpu
 
 QK_HEAD_DIM = 64
 
@@ -114,7 +114,7 @@ def qk_norm_rope(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, s
     return q, k
 
 
-@qk_norm_rope.register_fake
+@_fake(qk_norm_rope)
 def _(qkv, q_weight, k_weight, cos, sin, eps):
     b, n, _, h, d = qkv.shape
     return qkv.new_empty((b, n, h, d)), qkv.new_empty((b, n, h, d))
@@ -202,10 +202,23 @@ def qk_norm_rope_attention(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos:
     return out
 
 
-@qk_norm_rope_attention.register_fake
+@_fake(qk_norm_rope_attention)
 def _(qkv, q_weight, k_weight, cos, sin, eps):
     b, n, _, h, d = qkv.shape
     return qkv.new_empty((b, n, h, d))
+
+
+def _attention_fp32_recompute(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, sin: Tensor, eps: float):
+    """qk_norm_rope_attention_eager's function with the attention itself in fp32 matrix products and softmax
+    (softmax(q k^T / sqrt(64)) v, rounded once to qkv's dtype): the backward's recompute.  Plain products, not the
+    SDPA kernels, so torch.compile traces it (the ROCm flash-attention backward returns gradient strides its meta
+    function does not predict, which compiled graphs assert on)."""
+    q, k = qk_norm_rope_eager(qkv, q_weight, k_weight, cos, sin, eps)
+    v = qkv[:, :, 2]
+    q, k, v = (t.transpose(1, 2).float().contiguous() for t in (q, k, v))
+    kt = k.transpose(-1, -2).contiguous()
+    p = torch.softmax(torch.matmul(q, kt) * (QK_HEAD_DIM**-0.5), dim=-1)
+    return torch.matmul(p, v).to(qkv.dtype).transpose(1, 2)
 
 
 def _backward_qk_attention(ctx, grad):
@@ -213,7 +226,7 @@ def _backward_qk_attention(ctx, grad):
     need = ctx.needs_input_grad
     with torch.enable_grad():
         leaves = [t.detach().requires_grad_(bool(r)) for t, r in zip((qkv, q_weight, k_weight), need[:3])]
-        o = qk_norm_rope_attention_eager(leaves[0], leaves[1], leaves[2], cos, sin, ctx.eps)
+        o = _attention_fp32_recompute(leaves[0], leaves[1], leaves[2], cos, sin, ctx.eps)
         wanted = [t for t in leaves if t.requires_grad]
         got = torch.autograd.grad([o], wanted, [grad], allow_unused=True) if wanted else []
     it = iter(got)
@@ -245,7 +258,7 @@ def swiglu(x: Tensor) -> Tensor:
     return out
 
 
-@swiglu.register_fake
+@_fake(swiglu)
 def _(x):
     return x.new_empty((*x.shape[:-1], x.shape[-1] // 2))
 
@@ -314,7 +327,7 @@ def gate_add_norm_modulate(
     return d, y
 
 
-@gate_add_norm_modulate.register_fake
+@_fake(gate_add_norm_modulate)
 def _(z, a, gate, weight, shift, scale, eps):
     return torch.empty_like(z), torch.empty_like(z)
 
@@ -362,7 +375,7 @@ def gate_residual(d: Tensor, gate: Tensor, m: Tensor) -> Tensor:
     return out
 
 
-@gate_residual.register_fake
+@_fake(gate_residual)
 def _(d, gate, m):
     return torch.empty_like(d)
 
@@ -422,6 +435,6 @@ def block_tail(
     return dz, zn, y
 
 
-@block_tail.register_fake
+@_fake(block_tail)
 def _(z, a, gate, m, gamma, weight, shift, scale, eps):
     return torch.empty_like(z), torch.empty_like(z), torch.empty_like(z)

@@ -35,6 +35,7 @@ from .ops import (
     K,
     S,
     _check_weight,
+    _fake,
     _hi_geom,
     _launch_materialise,
     _launch_read_multi,
@@ -111,6 +112,30 @@ def _ws_backward(grad: Tensor, dzs: Sequence[Tensor] | None, gamma: Tensor, L: i
     return gdz, gg
 
 
+@torch.library.custom_op("jit_thc::ws_accumulate_backward", mutates_args=())
+def ws_accumulate_backward(grad: Tensor, dzs: list[Tensor], gamma: Tensor, L: int, want_dz: bool) -> tuple[list[Tensor], Tensor]:
+    """_ws_backward as an op (the triangular ops' autograd backwards call it, so torch.compile traces them as one
+    opaque node): ([gamma[i] * grad for i < L] or [] without want_dz, fp32 [L, C] sum grad * dzs[i] or an empty
+    tensor when dzs is empty)."""
+    gdz, gg = _ws_backward(grad, dzs if dzs else None, gamma, L, want_dz)
+    return (gdz if gdz is not None else []), (gg if gg is not None else grad.new_empty((0,), dtype=torch.float32))
+
+
+@_fake(ws_accumulate_backward)
+def _(grad: Tensor, dzs: list[Tensor], gamma: Tensor, L: int, want_dz: bool):
+    gdz = [torch.empty_like(grad) for _ in range(L)] if want_dz else []
+    gg = grad.new_empty((L, grad.shape[-1]) if dzs else (0,), dtype=torch.float32)
+    return gdz, gg
+
+
+def _ws_backward_op(grad: Tensor, dzs: Sequence[Tensor] | None, gamma: Tensor, L: int, want_dz):
+    """_ws_backward's (gdz list or None, gg or None) through the op.  `want_dz` is a bool, or the per-layer flags
+    of needs_input_grad for a list argument (any of them)."""
+    want_dz = any(want_dz) if isinstance(want_dz, (list, tuple)) else bool(want_dz)
+    gdz, gg = ws_accumulate_backward(grad, list(dzs) if dzs is not None else [], gamma, L, want_dz)
+    return (gdz if want_dz else None), (gg if dzs is not None else None)
+
+
 # ---------------------------------------------------------------------------
 # jit_thc::triangular_accumulate_traceable (stacked, any depth; :1922-2012)
 # ---------------------------------------------------------------------------
@@ -122,7 +147,7 @@ def triangular_accumulate_traceable(base: Tensor, dz_stack: Tensor, gamma: Tenso
     return _ws_forward(base, list(dz_stack.unbind(0)), gamma)
 
 
-@triangular_accumulate_traceable.register_fake
+@_fake(triangular_accumulate_traceable)
 def _(base: Tensor, dz_stack: Tensor, gamma: Tensor) -> Tensor:
     return torch.empty_like(base)
 
@@ -135,7 +160,7 @@ def triangular_accumulate_grad_dz_traceable(grad_out: Tensor, gamma: Tensor) -> 
     return torch.stack(gdz)
 
 
-@triangular_accumulate_grad_dz_traceable.register_fake
+@_fake(triangular_accumulate_grad_dz_traceable)
 def _(grad_out: Tensor, gamma: Tensor) -> Tensor:
     return grad_out.new_empty((gamma.shape[0], *grad_out.shape))
 
@@ -147,7 +172,7 @@ def triangular_accumulate_grad_gamma_traceable(grad_out: Tensor, dz_stack: Tenso
     return gg
 
 
-@triangular_accumulate_grad_gamma_traceable.register_fake
+@_fake(triangular_accumulate_grad_gamma_traceable)
 def _(grad_out: Tensor, dz_stack: Tensor, gamma: Tensor) -> Tensor:
     return grad_out.new_empty((gamma.shape[0], grad_out.shape[-1]), dtype=torch.float32)
 
@@ -162,7 +187,7 @@ def _backward_tri(ctx, grad_out):
     dz_stack, gamma = ctx.saved_tensors
     grad_out = grad_out.contiguous()
     need = ctx.needs_input_grad
-    gdz, gg = _ws_backward(grad_out, list(dz_stack.unbind(0)) if need[2] else None, gamma, gamma.shape[0], need[1])
+    gdz, gg = _ws_backward_op(grad_out, list(dz_stack.unbind(0)) if need[2] else None, gamma, gamma.shape[0], need[1])
     return (
         grad_out,
         torch.stack(gdz) if gdz is not None else None,
@@ -183,7 +208,7 @@ def triangular_accumulate_list(base: Tensor, dzs: list[Tensor], gamma: Tensor) -
     return _ws_forward(base, dzs, gamma)
 
 
-@triangular_accumulate_list.register_fake
+@_fake(triangular_accumulate_list)
 def _(base: Tensor, dzs: list[Tensor], gamma: Tensor) -> Tensor:
     return torch.empty_like(base)
 
@@ -199,7 +224,7 @@ def _backward_tri_list(ctx, grad_out):
     dzs, gamma = list(saved[: ctx.L]), saved[ctx.L]
     grad_out = grad_out.contiguous()
     need = ctx.needs_input_grad
-    gdz, gg = _ws_backward(grad_out, dzs if need[2] else None, gamma, ctx.L, need[1])
+    gdz, gg = _ws_backward_op(grad_out, dzs if need[2] else None, gamma, ctx.L, need[1])
     grad_gamma = None
     if gg is not None:
         if gamma.shape[0] > ctx.L:
@@ -317,32 +342,32 @@ for _name in (
     torch.library.impl(f"jit_thc::{_name}", "CPU")(_cpu_refusal(_name))
 
 
-@torch.library.register_fake("jit_thc::triangular_accumulate_b4_12_ptr_traceable")
+@_fake("jit_thc::triangular_accumulate_b4_12_ptr_traceable")
 def _(base, *args):
     return torch.empty_like(base)
 
 
-@torch.library.register_fake("jit_thc::triangular_accumulate_b4_12_ptr_grad_dz")
+@_fake("jit_thc::triangular_accumulate_b4_12_ptr_grad_dz")
 def _(grad_out, gamma):
     return grad_out.new_empty((12, *grad_out.shape))
 
 
-@torch.library.register_fake("jit_thc::triangular_accumulate_b4_12_ptr_grad_gamma")
+@_fake("jit_thc::triangular_accumulate_b4_12_ptr_grad_gamma")
 def _(grad_out, *args):
     return grad_out.new_empty((12, grad_out.shape[-1]), dtype=torch.float32)
 
 
-@torch.library.register_fake("jit_thc::triangular_accumulate_b4_12_ptr_active")
+@_fake("jit_thc::triangular_accumulate_b4_12_ptr_active")
 def _(base, *args):
     return torch.empty_like(base)
 
 
-@torch.library.register_fake("jit_thc::triangular_accumulate_b4_12_ptr_active_grad_dz")
+@_fake("jit_thc::triangular_accumulate_b4_12_ptr_active_grad_dz")
 def _(grad_out, gamma, active):
     return grad_out.new_empty((active, *grad_out.shape))
 
 
-@torch.library.register_fake("jit_thc::triangular_accumulate_b4_12_ptr_active_grad_gamma")
+@_fake("jit_thc::triangular_accumulate_b4_12_ptr_active_grad_gamma")
 def _(grad_out, *args):
     return grad_out.new_empty((12, grad_out.shape[-1]), dtype=torch.float32)
 
@@ -360,7 +385,7 @@ def _tri12_grads(ctx, grad_out) -> tuple:
     grad_out = grad_out.contiguous()
     need = ctx.needs_input_grad
     want_dz = any(need[1 : 1 + active])
-    gdz, gg = _ws_backward(grad_out, list(dzs[:active]) if need[13] else None, gamma, active, want_dz)
+    gdz, gg = _ws_backward_op(grad_out, list(dzs[:active]) if need[13] else None, gamma, active, want_dz)
     grad_dzs = (tuple(gdz) if gdz is not None else (None,) * active) + (None,) * (12 - active)
     grad_gamma = None
     if gg is not None:
@@ -408,9 +433,9 @@ def _make_active_op(active: int):
     torch.library.impl(f"jit_thc::{name}_grad_gamma", "CUDA")(lambda g, *a: _tri12_grad_gamma(g, a[:12], a[12], active))
     for suffix in ("", "_grad_dz", "_grad_gamma"):
         torch.library.impl(f"jit_thc::{name}{suffix}", "CPU")(_cpu_refusal(name + suffix))
-    torch.library.register_fake(f"jit_thc::{name}")(lambda base, *a: torch.empty_like(base))
-    torch.library.register_fake(f"jit_thc::{name}_grad_dz")(lambda g, gamma: g.new_empty((active, *g.shape)))
-    torch.library.register_fake(f"jit_thc::{name}_grad_gamma")(
+    _fake(f"jit_thc::{name}")(lambda base, *a: torch.empty_like(base))
+    _fake(f"jit_thc::{name}_grad_dz")(lambda g, gamma: g.new_empty((active, *g.shape)))
+    _fake(f"jit_thc::{name}_grad_gamma")(
         lambda g, *a: g.new_empty((12, g.shape[-1]), dtype=torch.float32)
     )
 
@@ -455,7 +480,7 @@ def all_base_b4_12_traceable(x0: Tensor, alpha_stack: Tensor) -> Tensor:
     return torch.stack(_bases(x0, alpha_stack))
 
 
-@all_base_b4_12_traceable.register_fake
+@_fake(all_base_b4_12_traceable)
 def _(x0: Tensor, alpha_stack: Tensor) -> Tensor:
     b, g, c = _hi_geom(x0, "x0")
     return x0.new_empty((alpha_stack.shape[0], b, g * g, c))
@@ -478,7 +503,7 @@ def all_base_b4_12_grad_x_traceable(grad_base: Tensor, alpha_stack: Tensor) -> T
     return out
 
 
-@all_base_b4_12_grad_x_traceable.register_fake
+@_fake(all_base_b4_12_grad_x_traceable)
 def _(grad_base: Tensor, alpha_stack: Tensor) -> Tensor:
     L, b, m, c = grad_base.shape
     h = int(round(m**0.5)) * S
@@ -494,7 +519,7 @@ def all_base_b4_12_grad_alpha_traceable(x0: Tensor, grad_base: Tensor, alpha_sta
     return _launch_weight_grad(x0, lows)
 
 
-@all_base_b4_12_grad_alpha_traceable.register_fake
+@_fake(all_base_b4_12_grad_alpha_traceable)
 def _(x0: Tensor, grad_base: Tensor, alpha_stack: Tensor) -> Tensor:
     return x0.new_empty((grad_base.shape[0], x0.shape[3], K), dtype=torch.float32)
 
@@ -522,7 +547,7 @@ def all_base_b4_12_split_traceable(x0: Tensor, alpha_stack: Tensor) -> list[Tens
     return _bases(x0, alpha_stack)
 
 
-@all_base_b4_12_split_traceable.register_fake
+@_fake(all_base_b4_12_split_traceable)
 def _(x0: Tensor, alpha_stack: Tensor) -> list[Tensor]:
     b, g, c = _hi_geom(x0, "x0")
     return [x0.new_empty((b, g * g, c)) for _ in range(alpha_stack.shape[0])]
@@ -537,7 +562,7 @@ def all_base_b4_12_split_grad_alpha_traceable(x0: Tensor, grad_base: Tensor) -> 
     return _launch_weight_grad(x0, lows)
 
 
-@all_base_b4_12_split_grad_alpha_traceable.register_fake
+@_fake(all_base_b4_12_split_grad_alpha_traceable)
 def _(x0: Tensor, grad_base: Tensor) -> Tensor:
     return x0.new_empty((grad_base.shape[0], x0.shape[3], K), dtype=torch.float32)
 
