@@ -2209,6 +2209,8 @@ int lthc_recur_bwd_sum(const void* g, const void* g_branch, const void* dz, cons
 #include "cast_many.inc"
 // LDS-staged backward tiles: the materialise backward and the single-pass interface backward.
 #include "bwd_tile.inc"
+
+#include "mat_bwd_mfma.inc"
 // Fused materialise backward (gdZ and gbeta from one pass over G).
 #include "materialise_bwd.inc"
 // Whole-interface entry points: recurrence prefix, read backward, interface forward / backward.
