@@ -61,13 +61,14 @@ def parse_args():
         "--profile",
         choices=[
             "materialise", "read", "recur", "read_multi", "weight_grad", "copy", "model", "train", "triangular",
-            "interface_c", "mat_bwd", "interface_bwd",
+            "interface_c", "mat_bwd", "interface_bwd", "interface_fwd",
         ],  # fmt: skip
         help="run only this kernel --steps times at the configured shape (for rocprofv3), plus one plain copy "
         "of X0 (a copy kernel of known size that calibrates the FETCH_SIZE / WRITE_SIZE counters); 'model' runs "
         "only the LTHC-B/4 forward leg (without the eager-interface comparison), 'train' only the interface fwd+bwd leg, 'triangular' only the non-shared "
         "interface forward leg, 'interface_c' only the whole-interface C calls at the training batch; 'mat_bwd' is "
-        "lthc_materialise_bwd and 'interface_bwd' lthc_interface_bwd (every workspace gradient given) at --batch",
+        "lthc_materialise_bwd, 'interface_bwd' lthc_interface_bwd (every workspace gradient given) and "
+        "'interface_fwd' lthc_interface_fwd (every dZ given) at the configured shape",
     )
     return p.parse_args()
 
@@ -866,7 +867,7 @@ def profile(args, ops, inputs, alpha, beta_stack, betas):
     x0, dzs = inputs
     z = ops.local_write_traceable(x0, alpha)
     gam = ops.lazy_gamma_stack(alpha, beta_stack)
-    if args.profile in ("mat_bwd", "interface_bwd"):
+    if args.profile in ("mat_bwd", "interface_bwd", "interface_fwd"):
         import ctypes
 
         from flowmatching_lthc_amd import _abi
@@ -886,6 +887,18 @@ def profile(args, ops, inputs, alpha, beta_stack, betas):
                     x0.data_ptr(), _abi.code(x0), _abi.ptr_array(dzs), _abi.ptr_array(betas), _abi.code(alpha),
                     _abi.ptr_array(gdz), gb.data_ptr(), B, G, 4, C, L, ws.data_ptr(), ws.numel(), sid,
                 ), "lthc_materialise_bwd")  # fmt: skip
+        elif args.profile == "interface_fwd":
+            ws = torch.empty((int(lib.lthc_interface_workspace_bytes(B, G, 4, C, L)),), device=x0.device,
+                             dtype=torch.uint8)  # fmt: skip
+            zs = [torch.empty_like(dzs[0]) for _ in range(L + 1)]
+            xl = torch.empty_like(x0)
+
+            def run():
+                _abi.check(lib.lthc_interface_fwd(
+                    x0.data_ptr(), _abi.code(x0), alpha.data_ptr(), _abi.ptr_array(betas), _abi.code(alpha),
+                    _abi.ptr_array(dzs), _abi.ptr_array(zs), xl.data_ptr(), B, G, 4, C, L, ws.data_ptr(),
+                    ws.numel(), sid,
+                ), "lthc_interface_fwd")  # fmt: skip
         else:  # G_L = x0; H_l tensors of their own (aliasing dZ_l would serve them from cache)
             ws = torch.empty((int(lib.lthc_interface_workspace_bytes(B, G, 4, C, L)),), device=x0.device,
                              dtype=torch.uint8)  # fmt: skip

@@ -466,9 +466,14 @@ __global__ __launch_bounds__(kBlock) void cell_mat_kernel(const void* __restrict
 // block into LDS as [layer][tap quad][channel] float4 rows, so a wavefront's
 // read of one quad is 64 consecutive 16-byte lanes (no bank conflicts).
 // Block = 4 wavefronts on one 64-channel slab, wavefront w on cell 4 b + w
-// of each grid step (gridDim.x * 4 cells): each dz run is
+// of each grid step (gridDim.x * 4 cells; NC = 2: cells 8 b + w and 8 b + w + 4
+// of gridDim.x * 8, when 8 | G): each dz run is
 // requested once per cell, where cell_mat_kernel's two tap groups request it
-// twice at these depths.  Same FMA order and roundings as cell_mat_kernel:
+// twice at these depths.  Two cells per wavefront and step (NC = 2) put twice
+// the loads in flight per wavefront and halve the LDS weight reads per cell
+// (one quad read serves both cells); their registers leave room for 4 layers
+// of weights in VGPRs, so 20 sit in LDS (80 KiB, two blocks per CU):
+// 2 % faster than NC = 1 at configuration 5's shape, bitwise equal.  Same FMA order and roundings as cell_mat_kernel:
 // acc = base, acc = fma(beta_l, dz_l, acc) for l = 0..L-1, one rounding.  When
 // L < LMAX (EXACT == false) the padding layers' dz and beta entries point at
 // layer 0 (filled in by the launcher, so the kernel indexes the pointer packs
@@ -476,13 +481,14 @@ __global__ __launch_bounds__(kBlock) void cell_mat_kernel(const void* __restrict
 // layer count is re-read in every cell iteration, so the compiler does not
 // hold a mask per layer across the loop (they spilled scalar registers).
 // ---------------------------------------------------------------------------
-template <int DT, int WDT, int LMAX, int LV, bool EXACT>
+template <int DT, int WDT, int LMAX, int LV, int NC, bool EXACT>
 __global__ __launch_bounds__(kBlock, 2) void cell_mat_deep_kernel(const void* __restrict__ base, PtrPack dz,
                                                                   PtrPack beta, void* __restrict__ out, int L,
                                                                   uint32_t ncells, int G, int C) {
   constexpr int ES = Fmt<DT>::bytes;
   constexpr int LD = LMAX - LV;  // layers whose weights sit in LDS
   static_assert(LD >= 1 && LV >= 1, "layer split");
+  static_assert(NC == 1 || NC == 2, "cells per wavefront and step");
   __shared__ float4 wl[LD][kK / 4][64];
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
@@ -503,53 +509,75 @@ __global__ __launch_bounds__(kBlock, 2) void cell_mat_deep_kernel(const void* __
     if (live) load_wvec<WDT, kK>(beta.p[l], static_cast<int64_t>(c0) * kK, bw[l]);
   }
   __syncthreads();
-  uint32_t cell = blockIdx.x * 4 + w;
+  uint32_t cell = blockIdx.x * (4 * NC) + w;
   if (!live || cell >= ncells) return;
   const uint32_t tap_b = C * ES;
   const uint32_t row_b = G * kS * tap_b;
-  const uint32_t P = gridDim.x * 4;
+  const uint32_t P = gridDim.x * 4 * NC;
   CellStride stride(P, cell, G, tap_b, row_b);
   const uint32_t step_z = P * tap_b;
+  // NC = 2: the wavefront's second cell is cell + 4, in the same cell row (the launcher requires 8 | G, so a block's
+  // run of 8 cells starting at a multiple of 8 stays in one row, and 8 | ncells, so both cells exist)
+  constexpr uint32_t kDn = 4;
+  const uint32_t dxo = kDn * kS * tap_b, dzo = kDn * tap_b;
   uint32_t xo = static_cast<uint32_t>((cell_hoff(cell, G, C) + c0) * ES);
   uint32_t zo = (cell * C + c0) * ES;
   for (; cell < ncells; cell += P, xo += stride.advance(), zo += step_z) {
-    Raw<DT, 1> xr[kK];
-    Raw<DT, 1> dr[LMAX];
+    Raw<DT, 1> xr[NC][kK];
+    Raw<DT, 1> dr[NC][LMAX];
 #pragma unroll
-    for (int k = 0; k < kK; ++k) load_at<DT, 1, true>(base, xo + (k / kS) * row_b + (k % kS) * tap_b, xr[k]);
+    for (int j = 0; j < NC; ++j)
 #pragma unroll
-    for (int l = 0; l < LMAX; ++l) load_at<DT, 1>(dz.p[l], zo, dr[l]);
+      for (int k = 0; k < kK; ++k)
+        load_at<DT, 1, true>(base, xo + j * dxo + (k / kS) * row_b + (k % kS) * tap_b, xr[j][k]);
+#pragma unroll
+    for (int j = 0; j < NC; ++j)
+#pragma unroll
+      for (int l = 0; l < LMAX; ++l) load_at<DT, 1>(dz.p[l], zo + j * dzo, dr[j][l]);
     LTHC_PHASE_BARRIER();
 
-    float acc[kK][1];
+    float acc[NC][kK][1];
 #pragma unroll
-    for (int k = 0; k < kK; ++k) unpack_raw<DT, 1>(xr[k], acc[k]);
+    for (int j = 0; j < NC; ++j)
+#pragma unroll
+      for (int k = 0; k < kK; ++k) unpack_raw<DT, 1>(xr[j][k], acc[j][k]);
     int Lc = L;
     if constexpr (!EXACT) asm volatile("" : "+s"(Lc));
 #pragma unroll
     for (int l = 0; l < LMAX; ++l) {
-      float d[1];
-      unpack_raw<DT, 1>(dr[l], d);
-      if constexpr (!EXACT) d[0] = l < Lc ? d[0] : 0.f;
+      float d[NC][1];
+#pragma unroll
+      for (int j = 0; j < NC; ++j) {
+        unpack_raw<DT, 1>(dr[j][l], d[j]);
+        if constexpr (!EXACT) d[j][0] = l < Lc ? d[j][0] : 0.f;
+      }
       if (l < LV) {
 #pragma unroll
-        for (int k = 0; k < kK; ++k) acc[k][0] = fmaf(bw[l < LV ? l : 0][k], d[0], acc[k][0]);
+        for (int k = 0; k < kK; ++k)
+#pragma unroll
+          for (int j = 0; j < NC; ++j) acc[j][k][0] = fmaf(bw[l < LV ? l : 0][k], d[j][0], acc[j][k][0]);
       } else {
 #pragma unroll
-        for (int q = 0; q < kK / 4; ++q) {
+        for (int q = 0; q < kK / 4; ++q) {  // one LDS read of a tap quad serves the NC cells
           const float4 b = wl[l >= LV ? l - LV : 0][q][lane];
-          acc[4 * q + 0][0] = fmaf(b.x, d[0], acc[4 * q + 0][0]);
-          acc[4 * q + 1][0] = fmaf(b.y, d[0], acc[4 * q + 1][0]);
-          acc[4 * q + 2][0] = fmaf(b.z, d[0], acc[4 * q + 2][0]);
-          acc[4 * q + 3][0] = fmaf(b.w, d[0], acc[4 * q + 3][0]);
+#pragma unroll
+          for (int j = 0; j < NC; ++j) {
+            acc[j][4 * q + 0][0] = fmaf(b.x, d[j][0], acc[j][4 * q + 0][0]);
+            acc[j][4 * q + 1][0] = fmaf(b.y, d[j][0], acc[j][4 * q + 1][0]);
+            acc[j][4 * q + 2][0] = fmaf(b.z, d[j][0], acc[j][4 * q + 2][0]);
+            acc[j][4 * q + 3][0] = fmaf(b.w, d[j][0], acc[j][4 * q + 3][0]);
+          }
         }
       }
+      if constexpr (NC == 2) LTHC_PHASE_BARRIER();  // one layer's LDS reads at a time (hoisted, they spilled)
     }
 #pragma unroll
-    for (int k = 0; k < kK; ++k) {
-      hold_f32<DT>(acc[k]);
-      store_at<DT, 1, true>(out, xo + (k / kS) * row_b + (k % kS) * tap_b, acc[k]);
-    }
+    for (int j = 0; j < NC; ++j)
+#pragma unroll
+      for (int k = 0; k < kK; ++k) {
+        hold_f32<DT>(acc[j][k]);
+        store_at<DT, 1, true>(out, xo + j * dxo + (k / kS) * row_b + (k % kS) * tap_b, acc[j][k]);
+      }
   }
 }
 
@@ -1652,22 +1680,27 @@ void launch_cell_mat(const void* base, const PtrPack& dz, const PtrPack& beta, v
 // Layers whose weights the deep materialisation keeps in VGPRs: 242 VGPRs at depth 24, two wavefronts per SIMD (with
 // 12 layers it spilled; 6 and 8 measured slower on MI355X).
 constexpr int kDeepRegLayers = 10;
+constexpr int kDeepRegLayers2 = 4;  // two cells per wavefront and step
 
 template <int DT, int WDT, int LMAX, bool EXACT>
 void launch_cell_mat_deep(const void* base, const PtrPack& dz, const PtrPack& beta, void* out, int L, int64_t ncells,
                           int G, int C, hipStream_t st) {
-  constexpr int LV = kDeepRegLayers;
-  const auto kernel = cell_mat_deep_kernel<DT, WDT, LMAX, LV, EXACT>;
-  static const int per_cu = resident_blocks(kernel);
-  const int slabs = (C + 63) / 64;
-  const int64_t per = grid_cells(static_cast<int64_t>(num_cus()) * per_cu * 4 / slabs, ncells, 4);
   PtrPack dp = dz, bp = beta;  // padding layers: layer 0's rows (contributing a selected 0)
   for (int l = L; l < LMAX; ++l) {
     dp.p[l] = dz.p[0];
     bp.p[l] = beta.p[0];
   }
-  kernel<<<dim3(static_cast<unsigned>(per / 4), slabs), kBlock, 0, st>>>(base, dp, bp, out, L,
-                                                                        static_cast<uint32_t>(ncells), G, C);
+  const int slabs = (C + 63) / 64;
+  auto run = [&](auto nc, auto lv) {
+    constexpr int NC = decltype(nc)::value, LV = decltype(lv)::value;
+    const auto kernel = cell_mat_deep_kernel<DT, WDT, LMAX, LV, NC, EXACT>;
+    static const int per_cu = resident_blocks(kernel);
+    const int64_t per = grid_cells(static_cast<int64_t>(num_cus()) * per_cu * 4 * NC / slabs, ncells, 4 * NC);
+    kernel<<<dim3(static_cast<unsigned>(per / (4 * NC)), slabs), kBlock, 0, st>>>(base, dp, bp, out, L,
+                                                                                 static_cast<uint32_t>(ncells), G, C);
+  };
+  if (G % 8 == 0) run(IC<2>{}, IC<kDeepRegLayers2>{});  // two cells per wavefront and step
+  else run(IC<1>{}, IC<kDeepRegLayers>{});
 }
 
 template <int DT, int WDT, int LMAX>

@@ -445,13 +445,14 @@ def test_edge_shapes_fp32(coracle, B, G, C, L):
     assert_f32(host(gam), coracle.Cgamma(d["alpha"], list(d["beta"])), tol=1e-6, what="gamma")
 
 
-# Depths 17-24 with a base run the deep whole-cell kernel (the weights of layers 10 and up staged in LDS): ragged
-# channel slabs (C % 64 != 0), workspace grids that its 4 cells per block do not divide, padded depths (L < 24) and
-# each activation / weight pair.
+# Depths 17-24 with a base run the deep whole-cell kernel (the weights of layers 10 and up staged in LDS; with 8 | G
+# two cells per wavefront and layers 4 and up in LDS): ragged channel slabs (C % 64 != 0), workspace grids that its
+# 4 cells per block do not divide, padded depths (L < 24) and each activation / weight pair.
 @pytest.mark.parametrize(
     "B,G,C,L,xdt,wdt",
     [(1, 2, 8, 17, F32, F32), (2, 6, 100, 24, BF16, F32), (1, 5, 68, 21, torch.float16, torch.float16),
-     (2, 16, 256, 23, BF16, BF16), (3, 3, 192, 24, F32, F32), (1, 4, 64, 19, torch.float16, F32)],
+     (2, 16, 256, 23, BF16, BF16), (3, 3, 192, 24, F32, F32), (1, 4, 64, 19, torch.float16, F32),
+     (1, 8, 100, 24, BF16, F32), (2, 8, 72, 24, F32, F32)],
 )  # fmt: skip
 def test_deep_materialise(coracle, B, G, C, L, xdt, wdt):
     d = cfg(B, G, C, L, seed=B * G + C + L)
