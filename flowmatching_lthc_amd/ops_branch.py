@@ -35,6 +35,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 from torch import Tensor
+from torch._subclasses.fake_tensor import is_fake
 
 from . import _abi
 from .ops import _fake, _mod_rows, _norm_weight, _on_device, _on_gpu
@@ -210,9 +211,10 @@ def _(qkv, q_weight, k_weight, cos, sin, eps):
 
 def _attention_fp32_recompute(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, cos: Tensor, sin: Tensor, eps: float):
     """qk_norm_rope_attention_eager's function with the attention itself in fp32 matrix products and softmax
-    (softmax(q k^T / sqrt(64)) v, rounded once to qkv's dtype): the backward's recompute.  Plain products, not the
-    SDPA kernels, so torch.compile traces it (the ROCm flash-attention backward returns gradient strides its meta
-    function does not predict, which compiled graphs assert on)."""
+    (softmax(q k^T / sqrt(64)) v, rounded once to qkv's dtype): the backward's recompute when torch.compile traces it.
+    Plain products, not the SDPA kernels: the ROCm flash-attention backward returns gradient strides its meta function
+    does not predict, which compiled graphs assert on.  Eager backwards keep the SDPA recompute (at B=64 the fp32
+    products made the LTHC-B/4 training step 25 % slower)."""
     q, k = qk_norm_rope_eager(qkv, q_weight, k_weight, cos, sin, eps)
     v = qkv[:, :, 2]
     q, k, v = (t.transpose(1, 2).float().contiguous() for t in (q, k, v))
@@ -221,12 +223,19 @@ def _attention_fp32_recompute(qkv: Tensor, q_weight: Tensor, k_weight: Tensor, c
     return torch.matmul(p, v).to(qkv.dtype).transpose(1, 2)
 
 
+def _traced(t: Tensor) -> bool:
+    """True while torch.compile traces the code (Dynamo, or AOTAutograd on fake tensors), False when it runs."""
+    return torch.compiler.is_compiling() or is_fake(t)
+
+
 def _backward_qk_attention(ctx, grad):
     qkv, q_weight, k_weight, cos, sin = ctx.saved_tensors
     need = ctx.needs_input_grad
+    # eager: the SDPA recompute (flash / efficient kernels); traced: fp32 products, whose strides the graph predicts
+    recompute = _attention_fp32_recompute if _traced(grad) else qk_norm_rope_attention_eager
     with torch.enable_grad():
         leaves = [t.detach().requires_grad_(bool(r)) for t, r in zip((qkv, q_weight, k_weight), need[:3])]
-        o = _attention_fp32_recompute(leaves[0], leaves[1], leaves[2], cos, sin, ctx.eps)
+        o = recompute(leaves[0], leaves[1], leaves[2], cos, sin, ctx.eps)
         wanted = [t for t in leaves if t.requires_grad]
         got = torch.autograd.grad([o], wanted, [grad], allow_unused=True) if wanted else []
     it = iter(got)
