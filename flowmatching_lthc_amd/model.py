@@ -933,7 +933,9 @@ MODEL_NAMES = _SHARED_READ_NAMES + tuple(_V2_NAMES)
 
 def build_model(name: str = "lthc_b4_velocity", **kwargs) -> nn.Module:
     """The registry of the public release (flowmatching_lthc/models/__init__.py:17-38): the LTHC-B/4 shared-read
-    fused-final12 model under its three names, and the four v2 models (``model_v2``)."""
+    fused-final12 model under its three names, and the four v2 models (``model_v2``).  The keys of the reference's
+    LocalTHC_JiT_models (local_thc.py:1801-1827) built here are taken too: the shared-read B/4 models, and the
+    per-block Triton-interface and TriangularLazy B/4 models (``model_triangular``)."""
     if name in _SHARED_READ_NAMES:
         return LocalTHC_JiT_models["SharedRead-FusedFinal12-LocalTHC-SharedAdaLN-JiT-B/4"](**kwargs)
     if name in _V2_NAMES:
@@ -942,7 +944,12 @@ def build_model(name: str = "lthc_b4_velocity", **kwargs) -> nn.Module:
         return LocalTHCV2_JiT_models[_V2_NAMES[name]](**kwargs)
     if name in LocalTHC_JiT_models:
         return LocalTHC_JiT_models[name](**kwargs)
-    raise ValueError(f"unknown model: {name}; available={MODEL_NAMES + tuple(LocalTHC_JiT_models)}")
+    from .model_triangular import PerBlock_JiT_models  # imported here: that module imports this one
+
+    if name in PerBlock_JiT_models:
+        return PerBlock_JiT_models[name](**kwargs)
+    available = MODEL_NAMES + tuple(LocalTHC_JiT_models) + tuple(PerBlock_JiT_models)
+    raise ValueError(f"unknown model: {name}; available={available}")
 
 
 @torch.no_grad()

@@ -464,11 +464,17 @@ def _check_alpha_stack(x0: Tensor, alpha_stack: Tensor) -> tuple[int, int, int, 
     return b, g, c, alpha_stack.shape[0]
 
 
-def _bases(x0: Tensor, alpha_stack: Tensor) -> list[Tensor]:
+def _bases(x0: Tensor, alpha_stack: Tensor, stacked: bool) -> Tensor | list[Tensor]:
+    """The L bases from one read_multi pass: written straight into one [L,B,M,C] tensor when stacked, else into
+    L separate [B,M,C] tensors."""
     _on_gpu(x0, alpha_stack)
     b, g, c, L = _check_alpha_stack(x0, alpha_stack)
     x0 = _prep(x0)
     alphas = list(_prep_w(alpha_stack, x0.dtype).unbind(0))
+    if stacked:
+        out = torch.empty((L, b, g * g, c), device=x0.device, dtype=x0.dtype)
+        _launch_read_multi(x0, alphas, list(out.unbind(0)))
+        return out
     outs = [torch.empty((b, g * g, c), device=x0.device, dtype=x0.dtype) for _ in range(L)]
     _launch_read_multi(x0, alphas, outs)
     return outs
@@ -477,7 +483,7 @@ def _bases(x0: Tensor, alpha_stack: Tensor) -> list[Tensor]:
 @torch.library.custom_op("jit_thc::all_base_b4_12_traceable", mutates_args=())
 def all_base_b4_12_traceable(x0: Tensor, alpha_stack: Tensor) -> Tensor:
     """[L,B,M,C] of R_{alpha_l}(x0) for every l, one pass over x0."""
-    return torch.stack(_bases(x0, alpha_stack))
+    return _bases(x0, alpha_stack, stacked=True)
 
 
 @_fake(all_base_b4_12_traceable)
@@ -544,7 +550,7 @@ torch.library.register_autograd(all_base_b4_12_traceable, _backward_all_base, se
 @torch.library.custom_op("jit_thc::all_base_b4_12_split_traceable", mutates_args=())
 def all_base_b4_12_split_traceable(x0: Tensor, alpha_stack: Tensor) -> list[Tensor]:
     """The L bases R_{alpha_l}(x0) as separate [B,M,C] tensors (one pass over x0)."""
-    return _bases(x0, alpha_stack)
+    return _bases(x0, alpha_stack, stacked=False)
 
 
 @_fake(all_base_b4_12_split_traceable)
