@@ -39,7 +39,7 @@ def modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor) -> torch
 
 class CastLinear(nn.Linear):
     """nn.Linear that, while the model's forward has converted every weight in one batched launch
-    (``SharedReadLocalTHCSharedAdaLNJiT._converted_weights``), multiplies by that (weight, bias) pair: the values
+    (``BatchedWeightCast._converted_weights``), multiplies by that (weight, bias) pair: the values
     autocast's own per-layer conversion would give.  Parameters and state-dict names are nn.Linear's."""
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
@@ -124,6 +124,19 @@ class VisionRotaryEmbeddingFast(nn.Module):
         return cache[1], cache[2]
 
 
+def _patch_rows(x: torch.Tensor, p: int, grid: tuple[int, int]) -> torch.Tensor:
+    """[B, Cin, H, W] -> [B, H/p, W/p, Cin*p*p]: each non-overlapping p x p patch as one row in (channel, row,
+    column) order, the layout of a kernel = stride = p convolution's weight.  Under CUDA autocast an fp32 image is
+    gathered and cast in one copy (the values autocast's cast of the gathered rows would give)."""
+    b, cin = x.shape[:2]
+    gh, gw = grid
+    view = x.reshape(b, cin, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5)
+    if x.is_cuda and x.dtype == torch.float32 and torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+        return torch.empty((b, gh, gw, cin, p, p), device=x.device, dtype=dt).copy_(view).view(b, gh, gw, cin * p * p)
+    return view.reshape(b, gh, gw, cin * p * p)
+
+
 class BottleneckPatchEmbedNHWC(nn.Module):
     """Conv patchify (in -> bottleneck, kernel = stride = patch) then 1x1 conv to C, NHWC out (local_thc.py:64-89)."""
 
@@ -151,22 +164,15 @@ class BottleneckPatchEmbedNHWC(nn.Module):
         # row, column order, the layout of its weight).  proj2 is a 1x1 convolution: a linear map over proj1's
         # channels.  As two GEMMs over patch rows in NHWC order the residual comes out NHWC directly, with
         # proj2's bias in the GEMM (no permute copy of the C-channel tensor, no separate bias pass).
-        b, cin = x.shape[:2]
-        p = self.patch_size[0]
-        gh, gw = self.grid_size
-        view = x.reshape(b, cin, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5)
-        if x.is_cuda and x.dtype == torch.float32 and torch.is_autocast_enabled("cuda"):
-            # autocast would cast the gathered fp32 patches to its dtype for proj1: gather and cast in one copy
-            # (the same round-to-nearest-even values)
-            dt = torch.get_autocast_dtype("cuda")
-            patches = torch.empty((b, gh, gw, cin, p, p), device=x.device, dtype=dt).copy_(view)
-            patches = patches.view(b, gh, gw, cin * p * p)
-        else:
-            patches = view.reshape(b, gh, gw, cin * p * p)
+        patches = _patch_rows(x, self.patch_size[0], self.grid_size)
         cast = self.__dict__.get("_cast")
         w1, w2, b2 = cast if cast is not None else (self.proj1.weight, self.proj2.weight, self.proj2.bias)
         h = F.linear(patches, w1.view(self.proj1.out_channels, -1))
         return F.linear(h, w2.view(self.proj2.out_channels, -1), b2)
+
+    def cast_targets(self) -> list[torch.Tensor] | None:
+        """The tensors forward() takes, in order, from a batched conversion set as ``_cast`` (None: no such form)."""
+        return [self.proj1.weight, self.proj2.weight, self.proj2.bias] if self.proj2.bias is not None else None
 
 
 class DirectPatchEmbedNHWC(nn.Module):
@@ -192,11 +198,14 @@ class DirectPatchEmbedNHWC(nn.Module):
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         if tuple(x.shape[-2:]) != self.img_size:
             raise ValueError(f"expected image size {self.img_size}, got {tuple(x.shape[-2:])}")
-        b, cin = x.shape[:2]
-        p = self.patch_size[0]
-        gh, gw = self.grid_size
-        patches = x.reshape(b, cin, gh, p, gw, p).permute(0, 2, 4, 1, 3, 5).reshape(b, gh, gw, cin * p * p)
-        return F.linear(patches, self.proj.weight.view(self.proj.out_channels, -1), self.proj.bias)
+        patches = _patch_rows(x, self.patch_size[0], self.grid_size)
+        cast = self.__dict__.get("_cast")
+        w, bias = cast if cast is not None else (self.proj.weight, self.proj.bias)
+        return F.linear(patches, w.view(self.proj.out_channels, -1), bias)
+
+    def cast_targets(self) -> list[torch.Tensor] | None:
+        """The tensors forward() takes, in order, from a batched conversion set as ``_cast`` (None: no such form)."""
+        return [self.proj.weight, self.proj.bias] if self.proj.bias is not None else None
 
 
 class TimestepEmbedder(nn.Module):
@@ -514,7 +523,132 @@ def migrate_lthc_state_dict_keys(state_dict: dict) -> dict:
     return out
 
 
-class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
+class BatchedWeightCast:
+    """Mixin for the models of this package: their inference forwards under autocast convert every linear and
+    patch-embedding weight in one launch instead of one conversion per layer."""
+
+    batched_weight_cast = True
+
+    def _conversion_targets(self) -> list[tuple[nn.Module, list[torch.Tensor]]]:
+        """Modules whose weights autocast would convert on every forward, with the tensors it would convert."""
+        out: list[tuple[nn.Module, list[torch.Tensor]]] = [
+            (m, [m.weight, m.bias] if m.bias is not None else [m.weight])
+            for m in self.modules()
+            if isinstance(m, CastLinear)
+        ]
+        pe = self.x_embedder
+        embed = pe.cast_targets() if hasattr(pe, "cast_targets") else None
+        if embed is not None:
+            out.append((pe, embed))
+        return out
+
+    @contextmanager
+    def _converted_weights(self):
+        """Under a bf16 / fp16 CUDA autocast without autograd and with fp32 parameters (inference), convert every
+        linear weight once, in one launch (ops.BatchedCast), for this forward: the values autocast's ~150
+        per-layer conversions would produce.  Otherwise (training, no autocast, 16-bit parameters) a no-op."""
+        targets = self._conversion_targets() if self.batched_weight_cast else []
+        dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
+        tensors = [t for _, ts in targets for t in ts]
+        usable = (
+            bool(tensors)
+            and dt in (torch.bfloat16, torch.float16)
+            and not torch.is_grad_enabled()
+            and all(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() for t in tensors)
+        )
+        bc = self.__dict__.get("_batched_cast") if usable else None
+        key = (dt, tuple((t.data_ptr(), t.numel()) for t in tensors)) if usable else None
+        if usable and (bc is None or bc.key != key):
+            if torch.cuda.is_current_stream_capturing():  # the table is built eagerly, outside a capture
+                usable = False
+            else:
+                bc = ops.BatchedCast(tensors, dt)
+                self.__dict__["_batched_cast"] = bc
+        if not usable:
+            yield
+            return
+        outs = bc()
+        i = 0
+        for m, ts in targets:
+            m.__dict__["_cast"] = tuple(outs[i : i + len(ts)])
+            i += len(ts)
+        try:
+            yield
+        finally:
+            for m, _ in targets:
+                m.__dict__.pop("_cast", None)
+
+
+def _standard_decoder(fl: nn.Module) -> bool:
+    """fl is this package's shared-AdaLN or per-block-AdaLN decoder with nothing replaced."""
+    return (
+        type(fl) in (FinalLayerSharedAdaLN, FinalLayer)
+        and "forward" not in fl.__dict__
+        and type(fl.norm_final) is RMSNorm
+        and fl.linear.bias is not None
+    )
+
+
+def decoder_records_grad(fl: nn.Module, x: torch.Tensor, cond: torch.Tensor) -> bool:
+    """Autograd would record decoder fl on x: then the eager decoder runs, since jit_thc::decoder_head's backward
+    replays the eager sequence and a training step with it took 5.5 ms longer (LTHC-B/4, B=64: 61.9 against
+    56.3 ms)."""
+    return torch.is_grad_enabled() and (
+        x.requires_grad or cond.requires_grad or any(p.requires_grad for p in fl.parameters())
+    )
+
+
+def _decoder_modulation(fl: nn.Module, cond: torch.Tensor) -> torch.Tensor:
+    """The [B, 2C] (shift, scale) a standard decoder applies for cond (local_thc.py:853-873)."""
+    return cond if type(fl) is FinalLayerSharedAdaLN else fl.adaLN_modulation(cond)
+
+
+def decode_output(model: nn.Module, x_hi: torch.Tensor, cond: torch.Tensor) -> torch.Tensor:
+    """unpatchify(final_layer(X, cond)) for X [B, H, H, C].  With a standard decoder, 16-bit X on the GPU, 4x4
+    patches and no autograd recording: RMSNorm, modulation, linear layer and unpatchify in one jit_thc::decoder_head
+    pass."""
+    fl = model.final_layer
+    b, hh, wh, c = x_hi.shape
+    x = x_hi.reshape(b, hh * wh, c)
+    fusable = getattr(model, "fused_decoder", True) and _standard_decoder(fl) and model.patch_size == 4
+    if fusable and not decoder_records_grad(fl, x, cond):
+        if ops.decoder_head_supported(x, fl.linear.weight):
+            t2 = _decoder_modulation(fl, cond)
+            if t2.dtype == x.dtype:
+                shift, scale = t2.chunk(2, dim=1)
+                lw, lb = fl.linear.__dict__.get("_cast") or (fl.linear.weight, fl.linear.bias)
+                return ops.decoder_head(x, fl.norm_final.weight, shift, scale, lw, lb, fl.norm_final.eps, hh, 4)
+            return model.unpatchify(FinalLayerSharedAdaLN.forward(fl, x, t2))
+    return model.unpatchify(fl(x, cond))
+
+
+def materialise_decode_output(
+    model: nn.Module, x0: torch.Tensor, dz_list: list[torch.Tensor], betas: list[torch.Tensor], cond: torch.Tensor
+) -> torch.Tensor | None:
+    """decode_output(model, x0 + sum_l P_{betas[l]}(dz_list[l]), cond) as one jit_thc::final_accumulate_decoder_head
+    pass, X_L never written, where that applies: no autograd, a standard decoder, 16-bit operands of one dtype on the
+    GPU and the pass's shapes.  None elsewhere: the caller materialises and decodes."""
+    fl = model.final_layer
+    if not (
+        getattr(model, "fused_materialise_decoder", True)
+        and getattr(model, "fused_decoder", True)
+        and not torch.is_grad_enabled()
+        and _standard_decoder(fl)
+        and all(dz.dtype == x0.dtype and dz.is_cuda for dz in dz_list)
+        and ops.materialise_decoder_supported(x0, dz_list, fl.linear.weight, model.patch_size)
+    ):
+        return None
+    t2 = _decoder_modulation(fl, cond)
+    if t2.dtype != x0.dtype:
+        return None
+    shift, scale = t2.chunk(2, dim=1)
+    lw, lb = fl.linear.__dict__.get("_cast") or (fl.linear.weight, fl.linear.bias)
+    return ops.final_accumulate_decoder_head(
+        x0, list(dz_list), list(betas), fl.norm_final.weight, shift, scale, lw, lb, fl.norm_final.eps, model.patch_size
+    )
+
+
+class SharedReadLocalTHCSharedAdaLNJiT(BatchedWeightCast, nn.Module):
     """LTHC JiT with a depth-shared read, per-layer writes and shared AdaLN (local_thc.py:883-1007, :1331-1394).
 
     forward_lazy: read X0 once, run the blocks on the workspace with the exact
@@ -655,6 +789,7 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
             and isinstance(fl.norm_final, RMSNorm)
             and fl.linear.bias is not None
             and self.patch_size == 4
+            and not decoder_records_grad(fl, x, t2)
             and ops.decoder_head_supported(x, fl.linear.weight)
         ):
             # RMSNorm + modulate + linear + unpatchify in one pass (jit_thc::decoder_head): y never reaches memory
@@ -808,54 +943,6 @@ class SharedReadLocalTHCSharedAdaLNJiT(nn.Module):
             return self.forward_lazy(x, t, y) if lazy else self.forward_naive(x, t, y)
         with self._converted_weights():
             return self.forward_lazy(x, t, y) if lazy else self.forward_naive(x, t, y)
-
-    def _conversion_targets(self) -> list[tuple[nn.Module, list[torch.Tensor]]]:
-        """Modules whose weights autocast would convert on every forward, with the tensors it would convert."""
-        out: list[tuple[nn.Module, list[torch.Tensor]]] = [
-            (m, [m.weight, m.bias] if m.bias is not None else [m.weight])
-            for m in self.modules()
-            if isinstance(m, CastLinear)
-        ]
-        pe = self.x_embedder
-        if pe.proj2.bias is not None:
-            out.append((pe, [pe.proj1.weight, pe.proj2.weight, pe.proj2.bias]))
-        return out
-
-    @contextmanager
-    def _converted_weights(self):
-        """Under a bf16 / fp16 CUDA autocast without autograd and with fp32 parameters (inference), convert every
-        linear weight once, in one launch (ops.BatchedCast), for this forward: the values autocast's ~150
-        per-layer conversions would produce.  Otherwise (training, no autocast, 16-bit parameters) a no-op."""
-        targets = self._conversion_targets() if self.batched_weight_cast else []
-        dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
-        tensors = [t for _, ts in targets for t in ts]
-        usable = (
-            bool(tensors)
-            and dt in (torch.bfloat16, torch.float16)
-            and not torch.is_grad_enabled()
-            and all(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous() for t in tensors)
-        )
-        bc = self.__dict__.get("_batched_cast") if usable else None
-        key = (dt, tuple((t.data_ptr(), t.numel()) for t in tensors)) if usable else None
-        if usable and (bc is None or bc.key != key):
-            if torch.cuda.is_current_stream_capturing():  # the table is built eagerly, outside a capture
-                usable = False
-            else:
-                bc = ops.BatchedCast(tensors, dt)
-                self.__dict__["_batched_cast"] = bc
-        if not usable:
-            yield
-            return
-        outs = bc()
-        i = 0
-        for m, ts in targets:
-            m.__dict__["_cast"] = tuple(outs[i : i + len(ts)])
-            i += len(ts)
-        try:
-            yield
-        finally:
-            for m, _ in targets:
-                m.__dict__.pop("_cast", None)
 
 
 class SharedReadFusedFinalLocalTHCSharedAdaLNJiT(SharedReadLocalTHCSharedAdaLNJiT):

@@ -28,6 +28,8 @@ side is 4 (the TriangularLazy forward keeps the reference's depth of 12).
 
 from __future__ import annotations
 
+from contextlib import nullcontext
+
 import torch
 import torch.nn as nn
 import torch.nn.functional as F
@@ -35,12 +37,14 @@ import torch.nn.functional as F
 from . import ops
 from . import ops_triangular as T
 from .local_thc import (
+    overridden,
     ChannelwiseLocalTokenHyperConnectionTriton,
     ChannelwiseLocalTokenHyperConnectionTritonFrozen,
     ChannelwiseLocalTokenHyperConnectionTritonReadAdd,
     ChannelwiseLocalTokenHyperConnectionTritonTraceable,
 )
 from .model import (
+    BatchedWeightCast,
     BottleneckPatchEmbedNHWC,
     CastLinear,
     DirectPatchEmbedNHWC,
@@ -49,6 +53,8 @@ from .model import (
     TimestepEmbedder,
     VisionRotaryEmbeddingFast,
     WorkspaceSharedAdaLNBranch,
+    decode_output,
+    materialise_decode_output,
     migrate_lthc_state_dict_keys,
 )
 
@@ -102,11 +108,17 @@ class LocalTHCTritonTraceableSharedAdaLNJiTBlock(LocalTHCTritonSharedAdaLNJiTBlo
     hyper_cls = ChannelwiseLocalTokenHyperConnectionTritonTraceable
 
 
-class LocalTHCTritonSharedAdaLNJiT(nn.Module):
-    """Per-block LocalTHC JiT with shared AdaLN heads (local_thc.py:876-1018, :1108-1111)."""
+class LocalTHCTritonSharedAdaLNJiT(BatchedWeightCast, nn.Module):
+    """Per-block LocalTHC JiT with shared AdaLN heads (local_thc.py:876-1018, :1108-1111).
+
+    Inference on the GPU takes this package's fused forms where they apply: every linear weight converted in one
+    launch under autocast, and the decoder as one pass (``fused_decoder``).
+    """
 
     block_cls: type[nn.Module] = LocalTHCTritonSharedAdaLNJiTBlock
     x_embedder_cls: type[nn.Module] = BottleneckPatchEmbedNHWC
+    fused_decoder = True
+    fused_materialise_decoder = True
 
     def __init__(
         self,
@@ -206,16 +218,24 @@ class LocalTHCTritonSharedAdaLNJiT(nn.Module):
         return self.shared_adaLN_modulation(c), self.shared_final_modulation(c)
 
     def _dense_output(self, x_hi: torch.Tensor, t2: torch.Tensor) -> torch.Tensor:
-        b, hh, wh, c = x_hi.shape
-        return self.unpatchify(self.final_layer(x_hi.reshape(b, hh * wh, c), t2))
+        """unpatchify(final_layer(X, t2)), one decoder pass where it applies."""
+        return decode_output(self, x_hi, t2)
 
-    def forward(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
-        """Per-block recurrence over the high-resolution stream (local_thc.py:1009-1018)."""
+    def _converted(self):
+        """The one-launch weight conversion, outside torch.compile (which fuses autocast's conversions itself)."""
+        return nullcontext() if torch.compiler.is_compiling() else self._converted_weights()
+
+    def _forward_per_block(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         t6, t2 = self._conditioning(t, y)
         x_hi = self.x_embedder(x)
         for block in self.blocks:
             x_hi = block(x_hi, t6, self.workspace_rope)
         return self._dense_output(x_hi, t2)
+
+    def forward(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
+        """Per-block recurrence over the high-resolution stream (local_thc.py:1009-1018)."""
+        with self._converted():
+            return self._forward_per_block(x, t, y)
 
 
 class LocalTHCDirectTritonSharedAdaLNJiT(LocalTHCTritonSharedAdaLNJiT):
@@ -298,16 +318,38 @@ class TriangularLazyFusedFinal12LocalTHCDirectTritonSharedAdaLNJiT(LocalTHCDirec
 
     def forward_naive(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         """The per-block recurrence (local_thc.py:1482-1484)."""
-        return super().forward(x, t, y)
+        with self._converted():
+            return self._forward_per_block(x, t, y)
+
+    def _weight_stacks(self, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+        """[L, C, 16] stacks of _expanded_alpha and _expanded_beta in dtype.  With neither hook replaced and one
+        pool group per channel, each stack is one softmax / one conversion over the stacked parameters: the same
+        values (the softmax is per row) in two launches instead of 24."""
+        simple = all(blk.hyper.group_dim == 1 and blk.hyper.use_softmax_write for blk in self.blocks)
+        base = TriangularLazyFusedFinal12LocalTHCDirectTritonSharedAdaLNJiT
+        if simple and not overridden(self, "_expanded_alpha", base):
+            logits = torch.stack([blk.hyper.read_logits for blk in self.blocks], dim=0)
+            alpha_stack = F.softmax(logits.float(), dim=-1).to(dtype=dtype)
+        else:
+            alpha_stack = torch.stack([self._expanded_alpha(blk, dtype) for blk in self.blocks], dim=0)
+        if simple and not overridden(self, "_expanded_beta", base):
+            beta_stack = torch.stack([blk.hyper.write_weight for blk in self.blocks], dim=0).to(dtype=dtype)
+        else:
+            beta_stack = torch.stack([self._expanded_beta(blk, dtype) for blk in self.blocks], dim=0)
+        return alpha_stack, beta_stack
 
     def forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         """local_thc.py:1486-1515.  alpha, beta and gamma are in x0's dtype, as the reference casts them; the unused
-        slots of each active-prefix sum hold one zero tensor."""
+        slots of each active-prefix sum hold one zero tensor.  With final_accumulate_reference and _dense_output
+        as they are, inference on the GPU materialises x_L inside the decoder's pass (never written)."""
         self._check_depth(len(self.blocks))
+        with self._converted():
+            return self._forward_lazy(x, t, y)
+
+    def _forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         t6, t2 = self._conditioning(t, y)
         x0 = self.x_embedder(x)
-        alpha_stack = torch.stack([self._expanded_alpha(block, x0.dtype) for block in self.blocks], dim=0)
-        beta_stack = torch.stack([self._expanded_beta(block, x0.dtype) for block in self.blocks], dim=0)
+        alpha_stack, beta_stack = self._weight_stacks(x0.dtype)
         base_stack = T.all_base_b4_12_traceable(x0, alpha_stack.contiguous())
         gamma = T.gamma_matrix(alpha_stack, beta_stack)
         zero_dz = torch.zeros_like(base_stack[0])
@@ -318,6 +360,11 @@ class TriangularLazyFusedFinal12LocalTHCDirectTritonSharedAdaLNJiT(LocalTHCDirec
                 slots = tuple(dz_list[j] if j < l else zero_dz for j in range(12))
                 z = T.triangular_accumulate_b4_12_ptr_active_traceable_ops[l - 1](z, *slots, gamma[l].contiguous())
             dz_list.append(block.branch(z, t6, self.workspace_rope))
+        base = TriangularLazyFusedFinal12LocalTHCDirectTritonSharedAdaLNJiT
+        if not any(overridden(self, h, base) for h in ("final_accumulate_reference", "_dense_output", "_expanded_beta")):
+            out = materialise_decode_output(self, x0, dz_list, list(beta_stack.unbind(0)), t2)
+            if out is not None:
+                return out
         return self._dense_output(self.final_accumulate_reference(x0, dz_list), t2)
 
     def forward(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor, use_lazy: bool = True) -> torch.Tensor:

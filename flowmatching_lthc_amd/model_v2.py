@@ -14,12 +14,16 @@ parameter names are the reference's, so its v2 checkpoints load unchanged.
 
 from __future__ import annotations
 
+from contextlib import nullcontext
+
 import torch
 import torch.nn as nn
 
 from . import ops
 from . import ops_triangular as T
+from .local_thc import overridden
 from .model import (
+    BatchedWeightCast,
     BottleneckPatchEmbedNHWC,
     CastLinear,
     DirectPatchEmbedNHWC,
@@ -30,6 +34,8 @@ from .model import (
     VisionRotaryEmbeddingFast,
     WorkspaceJiTBranch,
     WorkspaceSharedAdaLNBranch,
+    decode_output,
+    materialise_decode_output,
 )
 
 
@@ -110,8 +116,16 @@ class LocalTHCV2AdaLNBlock(nn.Module):
         return self.branch(z, c, rope)
 
 
-class _LocalTHCV2Base(nn.Module):
-    """The v2 B/4 model around the non-shared lazy schedule (lthc_v2/model.py:128-271)."""
+class _LocalTHCV2Base(BatchedWeightCast, nn.Module):
+    """The v2 B/4 model around the non-shared lazy schedule (lthc_v2/model.py:128-271).
+
+    Inference on the GPU takes this package's fused forms where they apply, with the hooks below left as they are:
+    every linear weight converted in one launch under autocast, and the materialisation fused with the decoder
+    (X_L never written; ``fused_materialise_decoder``) or the decoder as one pass (``fused_decoder``).
+    """
+
+    fused_decoder = True
+    fused_materialise_decoder = True
 
     block_cls: type[nn.Module]
     final_cls: type[nn.Module]
@@ -225,12 +239,26 @@ class _LocalTHCV2Base(nn.Module):
         return ops.final_accumulate_b4_12_traceable(x0, *dz_list, *betas)
 
     def _dense_output(self, x_hi: torch.Tensor, final_cond: torch.Tensor) -> torch.Tensor:
-        b, hh, wh, c = x_hi.shape
-        return self.unpatchify(self.final_layer(x_hi.reshape(b, hh * wh, c), final_cond))
+        """unpatchify(final_layer(X_L, final_cond)) (lthc_v2/model.py:248-251), one decoder pass where it applies."""
+        return decode_output(self, x_hi, final_cond)
 
     def _run_fused_schedule(self, x0: torch.Tensor, cond: torch.Tensor) -> torch.Tensor:
+        """X_L after the schedule's updates (lthc_v2/model.py:253-268)."""
+        return self._final_accumulate(x0, self._schedule_updates(x0, cond))
+
+    def _output(self, x0: torch.Tensor, cond: torch.Tensor, final_cond: torch.Tensor) -> torch.Tensor:
+        """_dense_output(_run_fused_schedule(x0, cond), final_cond); with none of the three hooks replaced, the
+        materialisation and the decoder in one pass where that applies."""
+        if any(overridden(self, h, _LocalTHCV2Base) for h in ("_run_fused_schedule", "_final_accumulate", "_dense_output")):
+            return self._dense_output(self._run_fused_schedule(x0, cond), final_cond)
+        dzs = self._schedule_updates(x0, cond)
+        betas = [blk.pool.beta(dtype=dzs[0].dtype).contiguous() for blk in self.blocks]
+        out = materialise_decode_output(self, x0, dzs, betas, final_cond)
+        return out if out is not None else self._dense_output(self._final_accumulate(x0, dzs), final_cond)
+
+    def _schedule_updates(self, x0: torch.Tensor, cond: torch.Tensor) -> list[torch.Tensor]:
         """For l = 0..11: z_l = R_l(x0) + sum_{j<l} gamma[l, j] dz_j (the active-prefix op of width l, the
-        unused dz slots filled with zeros), dz_l = the block's branch on z_l; then X_L (lthc_v2/model.py:253-268).
+        unused dz slots filled with zeros), dz_l = the block's branch on z_l; returns the dz_l.
         alpha, beta and gamma are in x0's dtype, as the reference casts them."""
         alphas = self._alpha_stack(dtype=x0.dtype)
         betas = self._beta_stack(dtype=x0.dtype)
@@ -244,7 +272,11 @@ class _LocalTHCV2Base(nn.Module):
                 slots = tuple(dzs[j] if j < l else zero_dz for j in range(12))
                 z = T.triangular_accumulate_b4_12_ptr_active_traceable_ops[l - 1](z, *slots, gamma[l].contiguous())
             dzs.append(self._branch_update(blk, z, cond))
-        return self._final_accumulate(x0, dzs)
+        return dzs
+
+    def _converted(self):
+        """The one-launch weight conversion, outside torch.compile (which fuses autocast's conversions itself)."""
+        return nullcontext() if torch.compiler.is_compiling() else self._converted_weights()
 
     def _branch_update(self, block: nn.Module, z: torch.Tensor, cond: torch.Tensor) -> torch.Tensor:
         raise NotImplementedError
@@ -268,11 +300,11 @@ class LocalTHCV2FusedFinal12SharedAdaLNJiT(_LocalTHCV2Base):
         return block.branch_update(z, cond, self.workspace_rope)
 
     def forward(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
-        c = self.t_embedder(t) + self.y_embedder(y)
-        t6 = self.shared_adaLN_modulation(c)
-        t2 = self.shared_final_modulation(c)
-        x_hi = self._run_fused_schedule(self.x_embedder(x), t6)
-        return self._dense_output(x_hi, t2)
+        with self._converted():
+            c = self.t_embedder(t) + self.y_embedder(y)
+            t6 = self.shared_adaLN_modulation(c)
+            t2 = self.shared_final_modulation(c)
+            return self._output(self.x_embedder(x), t6, t2)
 
 
 class LocalTHCV2FusedFinal12AdaLNJiT(_LocalTHCV2Base):
@@ -285,9 +317,9 @@ class LocalTHCV2FusedFinal12AdaLNJiT(_LocalTHCV2Base):
         return block.branch_update(z, cond, self.workspace_rope)
 
     def forward(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
-        c = self.t_embedder(t) + self.y_embedder(y)
-        x_hi = self._run_fused_schedule(self.x_embedder(x), c)
-        return self._dense_output(x_hi, c)
+        with self._converted():
+            c = self.t_embedder(t) + self.y_embedder(y)
+            return self._output(self.x_embedder(x), c, c)
 
 
 class LocalTHCV2DirectFusedFinal12SharedAdaLNJiT(LocalTHCV2FusedFinal12SharedAdaLNJiT):
