@@ -53,6 +53,12 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--model-batch", type=int, default=64, help="batch of the LTHC-B/4 forward leg (fwd img/s)")
     p.add_argument("--model-steps", type=int, default=10)
+    p.add_argument(
+        "--model-name",
+        default="lthc_b4_velocity",
+        help="build_model name of the model forward leg (the headline figure is lthc_b4_velocity; other names, e.g. "
+        "the TriangularLazy or v2 models, for --profile model)",
+    )
     p.add_argument("--no-model", action="store_true", help="skip the LTHC-B/4 forward leg")
     p.add_argument("--train-batch", type=int, default=64, help="batch of the interface fwd+bwd leg (configuration 3)")
     p.add_argument("--no-train", action="store_true", help="skip the interface fwd+bwd leg")
@@ -389,12 +395,13 @@ def model_forward(args, torch, dev, compare=True):
         del g, out
         return ms, same
 
-    ours = M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=0).to(dev).eval()
+    name = args.model_name
+    ours = M.randomize_parameters(M.build_model(name), seed=0).to(dev).eval()
     ms, out_ours = timed(ours)
     ms_graph, graph_same = graphed(ours, out_ours)
     # bf16 parameters under autocast, as the reference's benchmark holds the model (bench/benchmark_lthc_v2.py:28):
     # no per-forward weight casts
-    ours16 = M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=0).to(dev, torch.bfloat16).eval()
+    ours16 = M.randomize_parameters(M.build_model(name), seed=0).to(dev, torch.bfloat16).eval()
     ms16, out16 = timed(ours16)
     ms16_graph, graph16_same = graphed(ours16, out16)
     diff16 = float((out16.float() - out_ours.float()).abs().max() / out_ours.float().abs().max())
@@ -413,9 +420,9 @@ def model_forward(args, torch, dev, compare=True):
         "bf16_params_max_rel_diff_vs_fp32_params": diff16,
         "batch": B,
         "steps": args.model_steps,
-        "workload": "LTHC-B/4 velocity forward (lthc_b4_velocity), random-init weights, bf16 autocast",
+        "workload": f"{name} forward, random-init weights, bf16 autocast",
     }
-    if compare:
+    if compare and name == "lthc_b4_velocity":
         eager = eager_interface(M.randomize_parameters(M.build_model("lthc_b4_velocity"), seed=0).to(dev).eval(), torch)
         ms_eager, out_eager = timed(eager)
         res["torch_eager_interface_img_per_s"] = round(B / (ms_eager * 1e-3), 1)

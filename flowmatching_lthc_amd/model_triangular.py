@@ -313,7 +313,7 @@ class TriangularLazyFusedFinal12LocalTHCDirectTritonSharedAdaLNJiT(LocalTHCDirec
     def final_accumulate_reference(self, x0: torch.Tensor, dz_list: list[torch.Tensor]) -> torch.Tensor:
         """x_L = x0 + sum_l P_l(dz_l) in one pass, the write weights in dz's dtype (local_thc.py:1476-1480)."""
         self._check_depth(len(dz_list))
-        betas = [self._expanded_beta(block, dz_list[0].dtype).contiguous() for block in self.blocks]
+        betas = list(self._beta_stack(dz_list[0].dtype).unbind(0))
         return ops.final_accumulate_b4_12_traceable(x0, *dz_list, *betas)
 
     def forward_naive(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
@@ -321,22 +321,28 @@ class TriangularLazyFusedFinal12LocalTHCDirectTritonSharedAdaLNJiT(LocalTHCDirec
         with self._converted():
             return self._forward_per_block(x, t, y)
 
-    def _weight_stacks(self, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
-        """[L, C, 16] stacks of _expanded_alpha and _expanded_beta in dtype.  With neither hook replaced and one
-        pool group per channel, each stack is one softmax / one conversion over the stacked parameters: the same
-        values (the softmax is per row) in two launches instead of 24."""
-        simple = all(blk.hyper.group_dim == 1 and blk.hyper.use_softmax_write for blk in self.blocks)
+    def _simple_hyper(self, hook: str) -> bool:
+        """The hook is the class's own and every block has one pool group per channel and softmax read weights: the
+        stack of its results is one operation over the stacked parameters."""
         base = TriangularLazyFusedFinal12LocalTHCDirectTritonSharedAdaLNJiT
-        if simple and not overridden(self, "_expanded_alpha", base):
+        return not overridden(self, hook, base) and all(
+            blk.hyper.group_dim == 1 and blk.hyper.use_softmax_write for blk in self.blocks
+        )
+
+    def _alpha_stack(self, dtype: torch.dtype) -> torch.Tensor:
+        """[L, C, 16] of _expanded_alpha in dtype: one softmax over the stacked logits where that hook is the class's
+        own (the softmax is per row, so the values are the same; two launches instead of 24)."""
+        if self._simple_hyper("_expanded_alpha"):
             logits = torch.stack([blk.hyper.read_logits for blk in self.blocks], dim=0)
-            alpha_stack = F.softmax(logits.float(), dim=-1).to(dtype=dtype)
-        else:
-            alpha_stack = torch.stack([self._expanded_alpha(blk, dtype) for blk in self.blocks], dim=0)
-        if simple and not overridden(self, "_expanded_beta", base):
-            beta_stack = torch.stack([blk.hyper.write_weight for blk in self.blocks], dim=0).to(dtype=dtype)
-        else:
-            beta_stack = torch.stack([self._expanded_beta(blk, dtype) for blk in self.blocks], dim=0)
-        return alpha_stack, beta_stack
+            return F.softmax(logits.float(), dim=-1).to(dtype=dtype)
+        return torch.stack([self._expanded_alpha(blk, dtype) for blk in self.blocks], dim=0)
+
+    def _beta_stack(self, dtype: torch.dtype) -> torch.Tensor:
+        """[L, C, 16] of _expanded_beta in dtype: one conversion of the stacked parameters where that hook is the
+        class's own."""
+        if self._simple_hyper("_expanded_beta"):
+            return torch.stack([blk.hyper.write_weight for blk in self.blocks], dim=0).to(dtype=dtype)
+        return torch.stack([self._expanded_beta(blk, dtype) for blk in self.blocks], dim=0)
 
     def forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         """local_thc.py:1486-1515.  alpha, beta and gamma are in x0's dtype, as the reference casts them; the unused
@@ -349,7 +355,7 @@ class TriangularLazyFusedFinal12LocalTHCDirectTritonSharedAdaLNJiT(LocalTHCDirec
     def _forward_lazy(self, x: torch.Tensor, t: torch.Tensor, y: torch.Tensor) -> torch.Tensor:
         t6, t2 = self._conditioning(t, y)
         x0 = self.x_embedder(x)
-        alpha_stack, beta_stack = self._weight_stacks(x0.dtype)
+        alpha_stack, beta_stack = self._alpha_stack(x0.dtype), self._beta_stack(x0.dtype)
         base_stack = T.all_base_b4_12_traceable(x0, alpha_stack.contiguous())
         gamma = T.gamma_matrix(alpha_stack, beta_stack)
         zero_dz = torch.zeros_like(base_stack[0])

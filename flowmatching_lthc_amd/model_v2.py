@@ -225,17 +225,25 @@ class _LocalTHCV2Base(BatchedWeightCast, nn.Module):
             raise ValueError(f"token count {x.shape[1]} is not square")
         return x.reshape(x.shape[0], h, w, p, p, c).permute(0, 5, 1, 3, 2, 4).reshape(x.shape[0], c, h * p, w * p)
 
+    def _pool_stack(self, hook: str, dtype: torch.dtype) -> torch.Tensor:
+        """[L, C, 16] of every block's pool.alpha(dtype) or pool.beta(dtype).  Where no pool replaces the hook, the
+        parameters are stacked and converted once (the values of converting each; one launch instead of 12)."""
+        if any(overridden(blk.pool, hook, LinearChannelwisePool) for blk in self.blocks):
+            return torch.stack([getattr(blk.pool, hook)(dtype=dtype) for blk in self.blocks]).contiguous()
+        name = "read_weight" if hook == "alpha" else "write_weight"
+        return torch.stack([getattr(blk.pool, name) for blk in self.blocks]).to(dtype=dtype)
+
     def _alpha_stack(self, dtype: torch.dtype) -> torch.Tensor:
-        return torch.stack([blk.pool.alpha(dtype=dtype) for blk in self.blocks]).contiguous()
+        return self._pool_stack("alpha", dtype)
 
     def _beta_stack(self, dtype: torch.dtype) -> torch.Tensor:
-        return torch.stack([blk.pool.beta(dtype=dtype) for blk in self.blocks]).contiguous()
+        return self._pool_stack("beta", dtype)
 
     def _final_accumulate(self, x0: torch.Tensor, dz_list: list[torch.Tensor]) -> torch.Tensor:
         """X_L = x0 + sum_l P_l(dz_l), the write weights in dz's dtype (lthc_v2/model.py:242-246)."""
         if len(dz_list) != 12:
             raise ValueError("LocalTHC v2 fused final accumulation requires exactly 12 dz tensors")
-        betas = [blk.pool.beta(dtype=dz_list[0].dtype).contiguous() for blk in self.blocks]
+        betas = list(self._pool_stack("beta", dz_list[0].dtype).unbind(0))
         return ops.final_accumulate_b4_12_traceable(x0, *dz_list, *betas)
 
     def _dense_output(self, x_hi: torch.Tensor, final_cond: torch.Tensor) -> torch.Tensor:
@@ -252,7 +260,7 @@ class _LocalTHCV2Base(BatchedWeightCast, nn.Module):
         if any(overridden(self, h, _LocalTHCV2Base) for h in ("_run_fused_schedule", "_final_accumulate", "_dense_output")):
             return self._dense_output(self._run_fused_schedule(x0, cond), final_cond)
         dzs = self._schedule_updates(x0, cond)
-        betas = [blk.pool.beta(dtype=dzs[0].dtype).contiguous() for blk in self.blocks]
+        betas = list(self._pool_stack("beta", dzs[0].dtype).unbind(0))
         out = materialise_decode_output(self, x0, dzs, betas, final_cond)
         return out if out is not None else self._dense_output(self._final_accumulate(x0, dzs), final_cond)
 
