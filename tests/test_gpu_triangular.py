@@ -55,6 +55,11 @@ def check(got, ref, dtype, what):
         (BF16, F32, 2, 8, 1024, 13),
         (F32, F32, 1, 4, 36, 24),
         (BF16, BF16, 1, 4, 12, 7),
+        # the one-thread-per-run forward with two rows per thread (16-bit activations, fp32 gamma): even rows, and
+        # 27 rows, whose last thread has one row; then one row per thread in fp32 with an odd row count
+        (BF16, F32, 2, 16, 768, 4),
+        (BF16, F32, 3, 3, 768, 11),
+        (F32, F32, 1, 3, 64, 3),
     ],
 )
 def test_triangular_stacked_and_list_forward_backward(dt, gdt, B, G, C, L):
@@ -85,6 +90,35 @@ def test_triangular_stacked_and_list_forward_backward(dt, gdt, B, G, C, L):
     for l in range(L):
         assert torch.equal(ld[l].grad, td.grad[l])
     assert torch.equal(lg.grad[:L], tg.grad) and not lg.grad[L].any()
+
+
+@pytest.mark.parametrize("gdt,rows,L", [(BF16, 512, 11), (F32, 512, 11), (F32, 27, 5), (BF16, 27, 2)])
+def test_triangular_forward_kernels_bitwise_equal(gdt, rows, L):
+    """The forward's two kernels give the same bits: 16-byte aligned operands take the one-thread-per-run kernel,
+    operands 8 bytes off a 16-byte boundary (the ABI's 4-element rule still holds) the grid-stride kernel."""
+    print(f"case forward kernels gamma={gdt} rows={rows} L={L}", flush=True)
+    C = 768
+    gen = torch.Generator(device=DEV).manual_seed(rows + L)
+
+    def tensors(shift):  # bf16 [rows, C] views starting `shift` elements into their buffers
+        def one(scale):
+            buf = torch.empty(rows * C + 8, device=DEV, dtype=BF16)
+            v = buf[shift : shift + rows * C].view(1, rows, C)
+            v.copy_((torch.randn((1, rows, C), generator=gen, device=DEV) * scale).to(BF16))
+            return v
+
+        return one(1.0), [one(0.02) for _ in range(L)]
+
+    gamma = (torch.randn((L, C), generator=gen, device=DEV) * 0.1 + 1.0).to(gdt)
+    base, dzs = tensors(0)
+    base2, dzs2 = tensors(4)
+    base2.copy_(base)
+    for a, b in zip(dzs2, dzs):
+        a.copy_(b)
+    assert base.data_ptr() % 16 == 0 and base2.data_ptr() % 16 == 8
+    flat = T.triangular_accumulate_list(base, dzs, gamma)
+    strided = T.triangular_accumulate_list(base2, dzs2, gamma)
+    assert torch.equal(flat, strided)
 
 
 def test_triangular_grad_ops_direct():
