@@ -1201,6 +1201,10 @@ __global__ __launch_bounds__(256) void gamma_rounded_bwd_kernel(const void* __re
 // rows past the end are clamped to the last row and their results dropped).
 // ---------------------------------------------------------------------------
 constexpr int kRU = 4;
+// The backward's rows per phase: 2 measured faster than 4 at every size (B=64, C=768 -2.7 %; configuration 5 -1 %;
+// B=256 -8.5 %; gdz and the summed gradient bitwise equal), 8 slower except at C=1024.  Lanes of 8 channels
+// (16 bytes) with blocks of whole rows were slower at C=768.
+constexpr int kRUB = 2;
 
 template <int DT, typename Off>
 __global__ __launch_bounds__(256) void recur_fwd_kernel(const void* __restrict__ z, const void* __restrict__ dz,
@@ -1293,12 +1297,12 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
   }
   float s[4] = {0.f, 0.f, 0.f, 0.f};
   const int64_t re = active ? rows : 0;
-  const int64_t S = static_cast<int64_t>(4 * kRU) * gridDim.y;
-  for (int64_t r0 = static_cast<int64_t>(blockIdx.y) * 4 * kRU + (t >> 6); r0 < re; r0 += S) {
-    Raw<DT, 4> ar[kRU], dr[kRU], xr[HAS_ADD ? kRU : 1], br[HAS_G2 ? kRU : 1];
-    Off off[kRU];
+  const int64_t S = static_cast<int64_t>(4 * kRUB) * gridDim.y;
+  for (int64_t r0 = static_cast<int64_t>(blockIdx.y) * 4 * kRUB + (t >> 6); r0 < re; r0 += S) {
+    Raw<DT, 4> ar[kRUB], dr[kRUB], xr[HAS_ADD ? kRUB : 1], br[HAS_G2 ? kRUB : 1];
+    Off off[kRUB];
 #pragma unroll
-    for (int u = 0; u < kRU; ++u) {
+    for (int u = 0; u < kRUB; ++u) {
       const int64_t r = std::min(r0 + 4 * u, re - 1);
       off[u] = static_cast<Off>((r * C + c0) * ES);
       load_at<DT, 4, true>(g, off[u], ar[u]);
@@ -1308,7 +1312,7 @@ __global__ __launch_bounds__(256) void recur_bwd_kernel(const void* __restrict__
     }
     LTHC_PHASE_BARRIER();
 #pragma unroll
-    for (int u = 0; u < kRU; ++u) {
+    for (int u = 0; u < kRUB; ++u) {
       if (r0 + 4 * u < re) {
         float a[4], d[4], o4[4];
         unpack_raw<DT, 4>(ar[u], a);
@@ -1473,7 +1477,7 @@ int resident_blocks(K kernel) {
 const int64_t kRecurChunks = 1024;
 const int64_t kRecurBwdChunks = 256;
 
-int64_t recur_bwd_blocks_y(int64_t rows) { return std::min((rows + 4 * kRU - 1) / (4 * kRU), kRecurBwdChunks); }
+int64_t recur_bwd_blocks_y(int64_t rows) { return std::min((rows + 4 * kRUB - 1) / (4 * kRUB), kRecurBwdChunks); }
 
 // Deterministic reduction of nparts partial rows of n floats into out.
 void launch_reduce(const float* partial, int nparts, int64_t n, void* out, hipStream_t st, int odt = LTHC_F32) {

@@ -88,9 +88,9 @@ def test_workspace_sizes_are_consistent():
     n = _abi.weight_grad_workspace_bytes(256, 16, 4, 768, 12)
     assert n > 0 and n % (12 * 768 * 16 * 4) == 0
     assert _abi.weight_grad_workspace_bytes(0, 16, 4, 768, 12) == 0
-    # one partial row of C floats per row lane (4) of each block row; block rows = min(16-row chunks, 256)
+    # one partial row of C floats per block row; block rows = min(8-row chunks (4 row lanes x 2 rows), 256)
     assert _abi.recur_bwd_workspace_bytes(65536, 768) == 256 * 768 * 4
-    assert _abi.recur_bwd_workspace_bytes(100, 768) == 7 * 768 * 4
+    assert _abi.recur_bwd_workspace_bytes(100, 768) == 13 * 768 * 4
 
 
 def test_ops_refuse_cpu_tensors():
