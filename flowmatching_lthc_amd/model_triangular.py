@@ -331,7 +331,8 @@ class TriangularLazyFusedFinal12LocalTHCDirectTritonSharedAdaLNJiT(LocalTHCDirec
 
     def _alpha_stack(self, dtype: torch.dtype) -> torch.Tensor:
         """[L, C, 16] of _expanded_alpha in dtype: one softmax over the stacked logits where that hook is the class's
-        own (the softmax is per row, so the values are the same; two launches instead of 24)."""
+        own (the softmax is per row, so the values are the same; a stack, a softmax and a conversion instead of one
+        of each per block)."""
         if self._simple_hyper("_expanded_alpha"):
             logits = torch.stack([blk.hyper.read_logits for blk in self.blocks], dim=0)
             return F.softmax(logits.float(), dim=-1).to(dtype=dtype)
