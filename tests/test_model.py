@@ -296,3 +296,25 @@ def test_overridden_gamma_or_alpha_hooks_disable_the_one_launch_gammas():
     sr = Sub(8, 2, CONFIG["hidden_size"], CONFIG["hidden_size"])
     assert overridden(sr, "alpha", SharedLocalRead)
     assert not overridden(m.shared_read, "alpha", SharedLocalRead)
+
+
+def test_fused_decoder_only_where_autograd_does_not_record_it():
+    """The one-pass decoder head's backward replays the eager sequence (slower than the eager decoder's forward and
+    backward), so the models take it only where autograd records nothing: no-grad, or nothing that needs a gradient."""
+    fl = M.FinalLayerSharedAdaLN(32, 4, 3)
+    x = torch.randn(2, 64, 32)
+    t2 = torch.randn(2, 64)
+    assert M.decoder_records_grad(fl, x, t2)  # the decoder's parameters need gradients
+    with torch.no_grad():
+        assert not M.decoder_records_grad(fl, x, t2)
+    for p in fl.parameters():
+        p.requires_grad_(False)
+    assert not M.decoder_records_grad(fl, x, t2)
+    assert M.decoder_records_grad(fl, x.requires_grad_(), t2)
+    assert M.decoder_records_grad(fl, x.detach(), t2.requires_grad_())
+    # the per-block-AdaLN decoder counts its own AdaLN head
+    fa = M.FinalLayer(32, 4, 3)
+    for p in fa.parameters():
+        p.requires_grad_(False)
+    fa.adaLN_modulation[-1].weight.requires_grad_(True)
+    assert M.decoder_records_grad(fa, x.detach(), t2.detach())
