@@ -9,6 +9,8 @@ largest values, which the smaller configurations never reach.
   the interface backward (local_thc.py:1211-1223, 1325-1328, 1368-1372 differentiated; see test_gpu_full_size.py):
   the activation gradients on the same three samples, the weight gradients summed over the whole batch.  The bounds
   are the full-size tests': max |d| <= 1e-2 max|ref| (and mean |d| <= 4e-3 mean|ref| for activations).
+- the non-shared forward's triangular sums (ws_acc_fwd_flat_kernel, fp32 gamma) at the widest and narrowest width:
+  within one bf16 rounding of an fp64 sum, and exact where gamma is zero.
 """
 
 import numpy as np
@@ -114,3 +116,30 @@ def test_interface_bwd_metric_shape(inputs, coracle):
         pt = coracle.Cread_multi(g1, bs, G)
         for l in range(L):
             _check(f"d dZ_{l}[{b}]", ddz[l][b : b + 1], pt[l] + gam[l][None, None, :] * S[l + 1][b : b + 1], True)
+
+
+@pytest.mark.parametrize("active", [11, 1])
+def test_triangular_sums_metric_shape(active):
+    """The non-shared forward's triangular sum at the metric shape with fp32 gamma (the model's case under autocast:
+    the two-rows-per-thread kernel), against an fp64 sum on the GPU: within one bf16 rounding everywhere (the
+    kernel's fp32 fma chain is exact to well below it), and a zero gamma row returns the base bit for bit."""
+    from flowmatching_lthc_amd import ops_triangular as T
+
+    print(f"case triangular sum metric shape B={B} active={active}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(100 + active)
+    base = torch.randn((B, G * G, C), generator=gen, device=DEV).to(BF16)
+    dzs = [(torch.randn((B, G * G, C), generator=gen, device=DEV) * 0.02).to(BF16) for _ in range(active)]
+    gamma = torch.randn((12, C), generator=gen, device=DEV) * 0.1 + 1.0
+    gamma[:, 5] = 0.0  # channel 5: every term zero
+    slots = tuple(dzs[j] if j < active else torch.zeros_like(base) for j in range(12))
+    out = T.triangular_accumulate_b4_12_ptr_active_traceable_ops[active - 1](base, *slots, gamma)
+    assert out.dtype == BF16
+    assert torch.equal(out[..., 5], base[..., 5])
+    for b0 in range(0, B, 64):  # the fp64 reference in 64-sample slices
+        ref = base[b0 : b0 + 64].double()
+        for j in range(active):
+            ref += gamma[j].double() * dzs[j][b0 : b0 + 64].double()
+        got = out[b0 : b0 + 64].double()
+        d = (got - ref).abs()
+        assert d.max().item() <= 2e-2
+        assert bool((d <= 2.0**-8 * ref.abs() + 1e-5).all()), f"slice {b0}: beyond one bf16 rounding"
