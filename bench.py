@@ -779,7 +779,7 @@ def interface_train(args, torch, dev, ops, B=None, G=None, C=None, L=None, label
     W = B * G * G * C
     fused_bwd = 2 * (3 * T + 3 * L * W)
     # per-op compulsory bytes: materialise backward e(T + 2LW) (gdZ and gbeta from one read of G_L: the tile kernel
-    # bwd_tile_kernel), recurrence backward e(6LW) (per layer g, dz, the branch gradient and the materialisation's
+    # mbwd_mfma_kernel), recurrence backward e(6LW) (per layer g, dz, the branch gradient and the materialisation's
     # gradient in, two out), read backward e(3T + W) (G_L, gZ0 and X0 in, dX0 out)
     per_op_bwd = 2 * (4 * T + 8 * L * W + W)
     fwd_ms, step_ms = (graph_fwd, graph_step) if graph_error is None else (eager_fwd, eager_step)

@@ -3,7 +3,8 @@
 The materialisation and its backward pick a kernel by depth bucket: the whole-cell kernel with its weights in
 VGPRs for depths 1, 2, 4, 8 and 12 (exact and padded buckets), two tap groups for depths 13-16, the deep kernel
 with part of its weights in LDS for depths 17-24 with a base, and the block-range kernels above depth 24.  The
-backward's tile kernel has 4 wavefronts up to depth 12 and 8 above.  This sweep runs each depth from 1 to 25, plus
+backward's tile kernel has 4 wavefronts up to depth 12 and 8 above (with gbeta's layers in two 16-wide blocks of
+matrix-core columns above depth 16).  This sweep runs each depth from 1 to 25, plus
 33 and 48 (the largest the ABI takes), on one sample of the B/4 geometry (G = 16) at C = 256, with bf16 activations
 and fp32 weights (the released autocast run), fp16 activations and weights, and fp32 throughout, and checks:
 - lthc_materialise_fwd with and without a base against X0 + sum_l P_l dZ_l (local_thc.py:1368-1372;

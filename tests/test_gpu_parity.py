@@ -352,7 +352,8 @@ def test_config5_full_batch_materialise_bf16(coracle):
         (2, 16, 128, 1, torch.float16, torch.float16),
         (2, 8, 64, 4, F32, F32),
         (1, 32, 1024, 12, BF16, BF16),  # configuration 5's grid and width
-        (2, 16, 768, 13, BF16, F32),   # padded depth-24 bucket (four layer groups)
+        (2, 16, 768, 13, BF16, F32),   # padded depth-24 bucket (8 wavefronts; the second block of 16 layers empty)
+        (2, 16, 768, 18, torch.float16, torch.float16),  # the second block of 16 layers partly filled
         (1, 32, 1024, 24, BF16, F32),  # configuration 5's grid, width and depth
         (1, 8, 64, 25, BF16, F32),     # deeper than the fused kernel: the two separate passes
         (2, 4, 260, 3, BF16, F32),     # C not a multiple of 64: the two separate passes
