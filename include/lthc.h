@@ -136,8 +136,9 @@ int lthc_weight_grad(const void* high, const void* const* low, int x_dtype, floa
  * (local_thc_triton_kernels.py:512-680, 1800-1894): the same two results as
  * lthc_read_multi_fwd(G, beta) and lthc_weight_grad(G, dz), but G (the
  * largest tensor) is read once instead of twice.  gdz is bitwise equal to
- * lthc_read_multi_fwd's.  One LDS-staged tile kernel for 16-bit activations
- * with L <= 24, C % 64 == 0, G % 8 == 0 and 16-byte aligned dz and gdz; otherwise one
+ * lthc_read_multi_fwd's.  One LDS-staged tile kernel (gbeta on the matrix
+ * cores) for 16-bit activations with L <= 24, C % 64 == 0, G % 8 == 0 and
+ * 16-byte aligned dz and gdz; otherwise one
  * register kernel when L <= 24, C % 64 == 0 and G is below 4 GiB; otherwise
  * the two separate passes.  `dz`, `beta`, `gdz` are host arrays of L device
  * pointers; the workspace holds the fp32 partials.

@@ -53,6 +53,7 @@ def test_materialise_bwd_noalloc_equals_workspace_entry():
         (64, 16, 768, 12, torch.bfloat16),  # configuration 3 (the tile kernel)
         (2, 8, 128, 5, torch.float16),  # smaller, another depth bucket
         (3, 4, 64, 2, torch.float32),  # fp32: the older single-pass kernel
+        (4, 16, 256, 20, torch.bfloat16),  # the depth-24 bucket (8 wavefronts, two column blocks of layers)
         (64, 16, 768, 12, torch.bfloat16),  # the first shape again after the smaller calls
     ]
     for i, (B, G, C, L, dt) in enumerate(shapes):
